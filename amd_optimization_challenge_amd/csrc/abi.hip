@@ -1,0 +1,331 @@
+// extern "C" entry points of libmla_mi355x.so (declared in include/mla_mi355x.h).
+// Host code only: argument validation, workspace carve-up, launches.  Nothing
+// here allocates device memory or synchronizes the host.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <mutex>
+#include <string>
+
+#include "../../include/mla_mi355x.h"
+#include "mla_internal.hpp"
+
+namespace mla {
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(MLA_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+constexpr int kMaxDevices = 64;
+int g_cu_count[kMaxDevices] = {0};
+std::mutex g_cu_mutex;
+
+int cu_count(int* out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) return fail(MLA_ERR_UNSUPPORTED, "device ordinal %d too large", dev);
+  std::lock_guard<std::mutex> lock(g_cu_mutex);
+  if (g_cu_count[dev] == 0) {
+    int n = 0;
+    e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return hip_fail(e, "hipDeviceGetAttribute(MultiprocessorCount)");
+    g_cu_count[dev] = n;
+  }
+  *out = g_cu_count[dev];
+  return MLA_OK;
+}
+
+int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
+
+bool aligned(const void* p, int a) { return (reinterpret_cast<uintptr_t>(p) & (uintptr_t)(a - 1)) == 0; }
+
+int check_shape(int batch, int num_heads, int kv_mode) {
+  if (batch < 1) return fail(MLA_ERR_INVALID_ARGUMENT, "batch must be >= 1 (got %d)", batch);
+  if (num_heads != 16 && num_heads != 128)
+    return fail(MLA_ERR_UNSUPPORTED, "num_heads must be 16 or 128 (got %d)", num_heads);
+  if (kv_mode < MLA_KV_FP8 || kv_mode > MLA_KV_MXFP4K_FP8V)
+    return fail(MLA_ERR_INVALID_ARGUMENT, "unknown kv_mode %d", kv_mode);
+  if (num_heads == 128 && kv_mode == MLA_KV_MXFP4)
+    return fail(MLA_ERR_UNSUPPORTED, "kv_mode mxfp4 (fp4 V) is implemented for num_heads=16 only");
+  return MLA_OK;
+}
+
+}  // namespace
+
+int target_items_for(int num_heads, int kv_mode, int num_cu) {
+  // one resident work-group per item: H=16 fp8-V kernels fit two per CU
+  if (num_heads == 16 && kv_mode != MLA_KV_MXFP4) return 2 * num_cu;
+  return num_cu;
+}
+
+WsLayout workspace_layout(int batch, int num_heads, int kv_mode, int num_cu) {
+  WsLayout L;
+  L.target_items = target_items_for(num_heads, kv_mode, num_cu);
+  L.max_items = 2 * num_cu + batch;  // >= target + batch for every mode
+  int64_t off = 0;
+  L.quant_off = off;
+  off = align256(off + kQuantScratchBytes);
+  L.qfp8_off = off;
+  off = align256(off + (int64_t)batch * num_heads * kQKDim);
+  L.plan_off = off;
+  off = align256(off + (int64_t)(kPlanHeader + 4 * L.max_items + 2 * batch) * 4);
+  L.part_o_off = off;
+  off = align256(off + (int64_t)L.max_items * num_heads * kVDim * 4);
+  L.part_lse_off = off;
+  off = align256(off + (int64_t)L.max_items * num_heads * 4);
+  L.total = off;
+  return L;
+}
+
+namespace {
+
+int decode_params(const void* q_fp8, const float* q_scale, const void* k_cache, int64_t k_row_stride,
+                  const void* k_scales, int64_t k_scale_stride, const void* v_cache,
+                  int64_t v_row_stride, const float* kv_scale, const int32_t* kv_indptr,
+                  const int32_t* kv_indices, int batch, int num_heads, float sm_scale, int kv_mode,
+                  void* workspace, int64_t workspace_bytes, void* out, DecodeParams* p, WsLayout* L) {
+  int rc = check_shape(batch, num_heads, kv_mode);
+  if (rc) return rc;
+  int ncu = 0;
+  if ((rc = cu_count(&ncu))) return rc;
+  *L = workspace_layout(batch, num_heads, kv_mode, ncu);
+  if (workspace == nullptr || workspace_bytes < L->total)
+    return fail(MLA_ERR_WORKSPACE_TOO_SMALL, "workspace needs %lld bytes (got %lld)",
+                (long long)L->total, (long long)workspace_bytes);
+  if (!aligned(workspace, 256)) return fail(MLA_ERR_INVALID_ARGUMENT, "workspace must be 256-byte aligned");
+  if (!q_fp8 || !q_scale || !k_cache || !kv_indptr || !out)
+    return fail(MLA_ERR_INVALID_ARGUMENT, "null q/q_scale/k_cache/kv_indptr/out pointer");
+  if (!aligned(q_fp8, 16) || !aligned(k_cache, 16) || !aligned(out, 16))
+    return fail(MLA_ERR_INVALID_ARGUMENT, "q, k_cache and out must be 16-byte aligned");
+  if (!(sm_scale > 0.f)) return fail(MLA_ERR_INVALID_ARGUMENT, "sm_scale must be > 0");
+  const bool k_fp4 = kv_mode != MLA_KV_FP8;
+  const int64_t krow = k_fp4 ? kFp4RowBytes : kQKDim;
+  if (k_row_stride < krow || (k_row_stride % 16) != 0)
+    return fail(MLA_ERR_INVALID_ARGUMENT, "k_row_stride must be >= %lld and a multiple of 16 (got %lld)",
+                (long long)krow, (long long)k_row_stride);
+  if (k_fp4) {
+    if (!k_scales) return fail(MLA_ERR_INVALID_ARGUMENT, "mxfp4 K needs k_scales");
+    if (k_scale_stride < kMxBlocks)
+      return fail(MLA_ERR_INVALID_ARGUMENT, "k_scale_stride must be >= 18 (got %lld)", (long long)k_scale_stride);
+  }
+  if (kv_mode == MLA_KV_MXFP4K_FP8V) {
+    if (!v_cache || !aligned(v_cache, 16)) return fail(MLA_ERR_INVALID_ARGUMENT, "fp8 V cache missing or misaligned");
+    if (v_row_stride < kVDim || (v_row_stride % 16) != 0)
+      return fail(MLA_ERR_INVALID_ARGUMENT, "v_row_stride must be >= 512 and a multiple of 16");
+  }
+  if (kv_mode != MLA_KV_MXFP4 && !kv_scale) return fail(MLA_ERR_INVALID_ARGUMENT, "fp8 cache needs kv_scale");
+  char* ws = static_cast<char*>(workspace);
+  p->q_fp8 = static_cast<const uint8_t*>(q_fp8);
+  p->q_scale = q_scale;
+  p->k_cache = static_cast<const uint8_t*>(k_cache);
+  p->k_row_stride = k_row_stride;
+  p->k_scales = static_cast<const uint8_t*>(k_scales);
+  p->k_scale_stride = k_scale_stride;
+  p->v_cache = static_cast<const uint8_t*>(v_cache);
+  p->v_row_stride = v_row_stride;
+  p->kv_scale = kv_scale;
+  p->kv_indptr = kv_indptr;
+  p->kv_indices = kv_indices;
+  p->plan = reinterpret_cast<const int32_t*>(ws + L->plan_off);
+  p->part_o = reinterpret_cast<float*>(ws + L->part_o_off);
+  p->part_lse = reinterpret_cast<float*>(ws + L->part_lse_off);
+  p->out = static_cast<uint16_t*>(out);
+  p->sm_scale = sm_scale;
+  p->batch = batch;
+  p->num_heads = num_heads;
+  p->max_items = L->max_items;
+  return MLA_OK;
+}
+
+}  // namespace
+}  // namespace mla
+
+using namespace mla;
+
+extern "C" {
+
+const char* mla_last_error(void) { return g_last_error.c_str(); }
+
+int mla_abi_version(void) { return 1; }
+
+int mla_device_cu_count(int* num_cu) {
+  if (!num_cu) return fail(MLA_ERR_INVALID_ARGUMENT, "num_cu is null");
+  return cu_count(num_cu);
+}
+
+int mla_workspace_bytes(int batch, int num_heads, int kv_mode, int64_t* bytes) {
+  if (!bytes) return fail(MLA_ERR_INVALID_ARGUMENT, "bytes is null");
+  int rc = check_shape(batch, num_heads, kv_mode);
+  if (rc) return rc;
+  int ncu = 0;
+  if ((rc = cu_count(&ncu))) return rc;
+  *bytes = workspace_layout(batch, num_heads, kv_mode, ncu).total;
+  return MLA_OK;
+}
+
+int mla_quant_fp8_per_tensor(const void* x_bf16, int64_t n, void* out_fp8, float* out_scale,
+                             void* workspace, int64_t workspace_bytes, void* stream) {
+  if (n < 1) return fail(MLA_ERR_INVALID_ARGUMENT, "n must be >= 1");
+  if (!x_bf16 || !out_fp8 || !out_scale || !workspace)
+    return fail(MLA_ERR_INVALID_ARGUMENT, "null pointer argument");
+  if (!aligned(x_bf16, 16) || !aligned(out_fp8, 8) || !aligned(workspace, 16))
+    return fail(MLA_ERR_INVALID_ARGUMENT, "x must be 16-byte, out 8-byte, workspace 16-byte aligned");
+  if (workspace_bytes < kQuantScratchBytes)
+    return fail(MLA_ERR_WORKSPACE_TOO_SMALL, "workspace needs %lld bytes", (long long)kQuantScratchBytes);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  uint32_t* partials = static_cast<uint32_t*>(workspace);
+  int nb = 0;
+  hipError_t e = launch_amax(static_cast<const uint16_t*>(x_bf16), n, partials, &nb, nullptr, 0, 0, 0,
+                             nullptr, s);
+  if (e != hipSuccess) return hip_fail(e, "amax launch");
+  e = launch_quant_fp8(static_cast<const uint16_t*>(x_bf16), n, partials, nb,
+                       static_cast<uint8_t*>(out_fp8), out_scale, s);
+  if (e != hipSuccess) return hip_fail(e, "quant launch");
+  return MLA_OK;
+}
+
+int mla_pack_mxfp4(const void* x_bf16, int64_t rows, int cols, int64_t x_row_stride, void* packed,
+                   int64_t packed_row_stride, void* scales, int64_t scale_row_stride, void* stream) {
+  if (rows < 0 || cols < 32 || (cols % 32) != 0)
+    return fail(MLA_ERR_INVALID_ARGUMENT, "cols must be a positive multiple of 32 (got %d)", cols);
+  if (rows == 0) return MLA_OK;
+  if (!x_bf16 || !packed || !scales) return fail(MLA_ERR_INVALID_ARGUMENT, "null pointer argument");
+  if (x_row_stride < 2LL * cols || (x_row_stride % 16) != 0 || !aligned(x_bf16, 16))
+    return fail(MLA_ERR_INVALID_ARGUMENT, "x rows must be 16-byte aligned with stride >= 2*cols");
+  if (packed_row_stride < cols / 2 || (packed_row_stride % 16) != 0 || !aligned(packed, 16))
+    return fail(MLA_ERR_INVALID_ARGUMENT, "packed rows must be 16-byte aligned with stride >= cols/2");
+  if (scale_row_stride < cols / 32)
+    return fail(MLA_ERR_INVALID_ARGUMENT, "scale_row_stride must be >= cols/32");
+  hipError_t e = launch_pack_mxfp4(static_cast<const uint16_t*>(x_bf16), rows, cols, x_row_stride,
+                                   static_cast<uint8_t*>(packed), packed_row_stride,
+                                   static_cast<uint8_t*>(scales), scale_row_stride,
+                                   static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "pack launch");
+  return MLA_OK;
+}
+
+int mla_plan(const int32_t* kv_indptr, int batch, int num_heads, int kv_mode, void* workspace,
+             int64_t workspace_bytes, void* stream) {
+  int rc = check_shape(batch, num_heads, kv_mode);
+  if (rc) return rc;
+  if (!kv_indptr || !workspace) return fail(MLA_ERR_INVALID_ARGUMENT, "null pointer argument");
+  if (!aligned(workspace, 256)) return fail(MLA_ERR_INVALID_ARGUMENT, "workspace must be 256-byte aligned");
+  int ncu = 0;
+  if ((rc = cu_count(&ncu))) return rc;
+  WsLayout L = workspace_layout(batch, num_heads, kv_mode, ncu);
+  if (workspace_bytes < L.total)
+    return fail(MLA_ERR_WORKSPACE_TOO_SMALL, "workspace needs %lld bytes (got %lld)", (long long)L.total,
+                (long long)workspace_bytes);
+  int32_t* plan = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + L.plan_off);
+  hipError_t e = launch_plan(kv_indptr, batch, L.target_items, L.max_items, plan,
+                             static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "plan launch");
+  return MLA_OK;
+}
+
+int mla_decode(const void* q_fp8, const float* q_scale, const void* k_cache, int64_t k_row_stride,
+               const void* k_scales, int64_t k_scale_stride, const void* v_cache, int64_t v_row_stride,
+               const float* kv_scale, const int32_t* kv_indptr, const int32_t* kv_indices, int batch,
+               int num_heads, float sm_scale, int kv_mode, void* workspace, int64_t workspace_bytes,
+               void* out_bf16, void* stream) {
+  DecodeParams p;
+  WsLayout L;
+  int rc = decode_params(q_fp8, q_scale, k_cache, k_row_stride, k_scales, k_scale_stride, v_cache,
+                         v_row_stride, kv_scale, kv_indptr, kv_indices, batch, num_heads, sm_scale,
+                         kv_mode, workspace, workspace_bytes, out_bf16, &p, &L);
+  if (rc) return rc;
+  hipError_t e = launch_decode(p, kv_mode, L.max_items, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "decode launch");
+  return MLA_OK;
+}
+
+int mla_combine(int batch, int num_heads, void* workspace, int64_t workspace_bytes, void* out_bf16,
+                void* stream) {
+  int rc = check_shape(batch, num_heads, MLA_KV_FP8);
+  if (rc) return rc;
+  if (!workspace || !out_bf16) return fail(MLA_ERR_INVALID_ARGUMENT, "null pointer argument");
+  int ncu = 0;
+  if ((rc = cu_count(&ncu))) return rc;
+  WsLayout L = workspace_layout(batch, num_heads, MLA_KV_FP8, ncu);
+  if (workspace_bytes < L.total)
+    return fail(MLA_ERR_WORKSPACE_TOO_SMALL, "workspace needs %lld bytes (got %lld)", (long long)L.total,
+                (long long)workspace_bytes);
+  char* ws = static_cast<char*>(workspace);
+  DecodeParams p = {};
+  p.plan = reinterpret_cast<const int32_t*>(ws + L.plan_off);
+  p.part_o = reinterpret_cast<float*>(ws + L.part_o_off);
+  p.part_lse = reinterpret_cast<float*>(ws + L.part_lse_off);
+  p.out = static_cast<uint16_t*>(out_bf16);
+  p.batch = batch;
+  p.num_heads = num_heads;
+  p.max_items = L.max_items;
+  hipError_t e = launch_combine(p, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "combine launch");
+  return MLA_OK;
+}
+
+int mla_decode_fwd(const void* q_bf16, const void* k_cache, int64_t k_row_stride, const void* k_scales,
+                   int64_t k_scale_stride, const void* v_cache, int64_t v_row_stride,
+                   const float* kv_scale, const int32_t* kv_indptr, const int32_t* kv_indices, int batch,
+                   int num_heads, float sm_scale, int kv_mode, void* workspace,
+                   int64_t workspace_bytes, void* out_bf16, void* stream) {
+  if (!q_bf16 || !aligned(q_bf16, 16)) return fail(MLA_ERR_INVALID_ARGUMENT, "q must be non-null and 16-byte aligned");
+  if (!workspace) return fail(MLA_ERR_INVALID_ARGUMENT, "null workspace");
+  char* ws = static_cast<char*>(workspace);
+  int rc = check_shape(batch, num_heads, kv_mode);
+  if (rc) return rc;
+  int ncu = 0;
+  if ((rc = cu_count(&ncu))) return rc;
+  WsLayout L0 = workspace_layout(batch, num_heads, kv_mode, ncu);
+  if (workspace_bytes < L0.total)
+    return fail(MLA_ERR_WORKSPACE_TOO_SMALL, "workspace needs %lld bytes (got %lld)", (long long)L0.total,
+                (long long)workspace_bytes);
+  uint8_t* q_fp8 = reinterpret_cast<uint8_t*>(ws + L0.qfp8_off);
+  float* q_scale = reinterpret_cast<float*>(ws + L0.quant_off + 4096);
+  DecodeParams p;
+  WsLayout L;
+  rc = decode_params(q_fp8, q_scale, k_cache, k_row_stride, k_scales, k_scale_stride, v_cache,
+                     v_row_stride, kv_scale, kv_indptr, kv_indices, batch, num_heads, sm_scale, kv_mode,
+                     workspace, workspace_bytes, out_bf16, &p, &L);
+  if (rc) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t n = (int64_t)batch * num_heads * kQKDim;
+  uint32_t* partials = reinterpret_cast<uint32_t*>(ws + L.quant_off);
+  int nb = 0;
+  hipError_t e = launch_amax(static_cast<const uint16_t*>(q_bf16), n, partials, &nb, kv_indptr, batch,
+                             L.target_items, L.max_items,
+                             reinterpret_cast<int32_t*>(ws + L.plan_off), s);
+  if (e != hipSuccess) return hip_fail(e, "amax+plan launch");
+  e = launch_quant_fp8(static_cast<const uint16_t*>(q_bf16), n, partials, nb, q_fp8, q_scale, s);
+  if (e != hipSuccess) return hip_fail(e, "quant launch");
+  e = launch_decode(p, kv_mode, L.max_items, s);
+  if (e != hipSuccess) return hip_fail(e, "decode launch");
+  e = launch_combine(p, s);
+  if (e != hipSuccess) return hip_fail(e, "combine launch");
+  return MLA_OK;
+}
+
+int mla_selftest(int which, const void* in, void* out, void* stream) {
+  if (!in || !out) return fail(MLA_ERR_INVALID_ARGUMENT, "null pointer argument");
+  hipError_t e = launch_selftest(which, in, out, static_cast<hipStream_t>(stream));
+  if (e == hipErrorInvalidValue) return fail(MLA_ERR_INVALID_ARGUMENT, "unknown selftest %d", which);
+  if (e != hipSuccess) return hip_fail(e, "selftest launch");
+  return MLA_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,145 @@
+// Shared device helpers and host-visible layout constants for the gfx950 MLA
+// decode library.  Everything here is CDNA4-specific: 64-lane waves, the
+// gfx950 f8f6f4 MFMA family and the OCP fp8/fp4 formats gfx950 uses natively.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mla {
+
+constexpr int kQKDim = 576;       // 512 latent + 64 rope
+constexpr int kVDim = 512;        // latent part, used as V
+constexpr int kFp4RowBytes = 288; // 576 e2m1 values, two per byte
+constexpr int kMxBlocks = 18;     // 576 / 32 e8m0 scales per row
+constexpr int kTile = 64;         // tokens staged per LDS tile
+
+// ---- plan layout (int32 words inside the workspace) -------------------------
+// header[0] = number of work items, [1] = chunk, [2] = total tokens, [3] = batch
+// items: int4 {batch, token_begin, token_end, partial_slot (-1 = final)}
+// batch_info: int2 {first item, item count}
+constexpr int kPlanHeader = 16;
+
+// ---- kernel parameter block --------------------------------------------------
+struct DecodeParams {
+  const uint8_t* q_fp8;      // [B, H, 576]
+  const float* q_scale;      // [1]
+  const uint8_t* k_cache;    // fp8 rows or packed fp4 rows
+  int64_t k_row_stride;      // bytes
+  const uint8_t* k_scales;   // e8m0 rows (fp4 K)
+  int64_t k_scale_stride;    // bytes
+  const uint8_t* v_cache;    // fp8 rows (fp8 V from a separate cache)
+  int64_t v_row_stride;      // bytes
+  const float* kv_scale;     // [1] fp8 per-tensor scale (fp8 K and/or V)
+  const int32_t* kv_indptr;  // [B+1]
+  const int32_t* kv_indices; // [T] or nullptr (identity)
+  const int32_t* plan;       // plan block (see above)
+  float* part_o;             // [max_items, H, 512]
+  float* part_lse;           // [max_items, H]  (log2 domain)
+  uint16_t* out;             // [B, H, 512] bf16
+  float sm_scale;
+  int batch;
+  int num_heads;
+  int max_items;
+};
+
+// ---- vector types ------------------------------------------------------------
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// 16-byte streaming load (read once; do not keep in cache)
+__device__ __forceinline__ uint4 ldg16_nt(const void* p) {
+  u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
+// ---- bf16 / fp8 scalar conversions (bit exact, no fast math) ----------------
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) {
+  return __uint_as_float(h << 16);
+}
+
+// Round-to-nearest-even f32 -> bf16 bits for finite inputs.
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+// Round-to-nearest-even f32 -> OCP e4m3fn code for |f| <= 448.
+__device__ __forceinline__ uint32_t f32_to_e4m3fn(float f) {
+  uint32_t u = __float_as_uint(f);
+  uint32_t sign = (u >> 24) & 0x80u;
+  u &= 0x7FFFFFFFu;
+  float a = __uint_as_float(u);
+  uint32_t code;
+  if (a < 0.015625f) {  // below 2^-6: subnormal grid of 2^-9, k = 8 is 2^-6
+    code = (uint32_t)__builtin_rintf(a * 512.0f);
+  } else {
+    uint32_t odd = (u >> 20) & 1u;
+    u += 0x7FFFFu + odd;
+    code = (u >> 20) - (120u << 3);
+  }
+  return sign | code;
+}
+
+// ---- wave helpers ------------------------------------------------------------
+__device__ __forceinline__ float shfl_xor_f(float v, int mask) {
+  return __shfl_xor(v, mask, 64);
+}
+
+// ---- MFMA wrappers (gfx950) --------------------------------------------------
+// D = A * B + C, A: 16 x 128 fp8, B: 128 x 16 fp8 (lane l: row/col l%16,
+// K elements 32*(l/16) .. +31), D: lane l holds column l%16, rows 4*(l/16)+r.
+__device__ __forceinline__ v4f mfma16_f8(v8i a, v8i b, v4f c) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+// Same shape, A = e2m1 (first four dwords) with an e8m0 scale per lane
+// (one per 32 K values), B = fp8 with unit scale.
+__device__ __forceinline__ v4f mfma16_f4f8(v8i a, int a_scale, v8i b, v4f c) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 4, 0, 0, a_scale, 0, 127);
+}
+// D = A * B + C, A: 32 x 64 fp8, B: 64 x 32 fp8 (lane l: row/col l%32, K
+// elements 32*(l/32) .. +31); D: lane l holds column l%32, rows
+// 8*(r/4) + 4*(l/32) + r%4 for r = 0..15.
+__device__ __forceinline__ v16f mfma32_f8(v8i a, v8i b, v16f c) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+__device__ __forceinline__ v16f mfma32_f4f8(v8i a, int a_scale, v8i b, v16f c) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 4, 0, 0, a_scale, 0, 127);
+}
+// 16x16x32 fp8 (K = 32): lane l: row/col l%16, K elements 8*(l/16) .. +7.
+__device__ __forceinline__ v4f mfma16x32_f8(long a, long b, v4f c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(a, b, c, 0, 0, 0);
+}
+// 16x16x32 bf16 (K = 32): lane l: row/col l%16, K elements 8*(l/16) .. +7.
+__device__ __forceinline__ v4f mfma16x32_bf16(v8bf a, v8bf b, v4f c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// Pack four floats (each in [0, 448]) into four e4m3fn bytes, element i in byte i.
+__device__ __forceinline__ uint32_t pack4_fp8(float a, float b, float c, float d) {
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+  return (uint32_t)w;
+}
+
+// Byte-transpose of a 4x4 byte block: y[e] byte r = x[r] byte e.
+__device__ __forceinline__ void transpose4x4_bytes(uint32_t x0, uint32_t x1, uint32_t x2,
+                                                   uint32_t x3, uint32_t y[4]) {
+  // pair rows (0,1) and (2,3) byte-interleaved, then merge halves
+  uint32_t t01lo = __builtin_amdgcn_perm(x1, x0, 0x05010400u);  // x0b0 x1b0 x0b1 x1b1
+  uint32_t t01hi = __builtin_amdgcn_perm(x1, x0, 0x07030602u);  // x0b2 x1b2 x0b3 x1b3
+  uint32_t t23lo = __builtin_amdgcn_perm(x3, x2, 0x05010400u);
+  uint32_t t23hi = __builtin_amdgcn_perm(x3, x2, 0x07030602u);
+  y[0] = __builtin_amdgcn_perm(t23lo, t01lo, 0x05040100u);  // t01lo b0 b1, t23lo b0 b1
+  y[1] = __builtin_amdgcn_perm(t23lo, t01lo, 0x07060302u);
+  y[2] = __builtin_amdgcn_perm(t23hi, t01hi, 0x05040100u);
+  y[3] = __builtin_amdgcn_perm(t23hi, t01hi, 0x07060302u);
+}
+
+}  // namespace mla

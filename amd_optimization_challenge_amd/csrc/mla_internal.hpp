@@ -1,0 +1,50 @@
+// Host-side declarations shared between the library's translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "mla_common.hpp"
+
+namespace mla {
+
+// Blocks used by the amax pass (also the number of partial maxima written).
+constexpr int kAmaxMaxBlocks = 1024;
+// Byte size of the quantizer scratch area at the front of every workspace.
+constexpr int64_t kQuantScratchBytes = 8192;
+
+// Workspace carve-up for one decode call; every offset is 256-byte aligned.
+struct WsLayout {
+  int64_t quant_off;   // kQuantScratchBytes: amax partials [1024] u32, q_scale f32 at +4096
+  int64_t qfp8_off;    // B*H*576 bytes
+  int64_t plan_off;    // (kPlanHeader + 4*max_items + 2*B) int32
+  int64_t part_o_off;  // max_items*H*512 f32
+  int64_t part_lse_off;// max_items*H f32
+  int64_t total;
+  int max_items;
+  int target_items;
+};
+
+int target_items_for(int num_heads, int kv_mode, int num_cu);
+WsLayout workspace_layout(int batch, int num_heads, int kv_mode, int num_cu);
+
+// quant.hip
+hipError_t launch_amax(const uint16_t* x, int64_t n, uint32_t* partials, int* nblocks,
+                       const int32_t* kv_indptr, int batch, int target_items, int max_items,
+                       int32_t* plan, hipStream_t stream);
+hipError_t launch_quant_fp8(const uint16_t* x, int64_t n, const uint32_t* partials, int nblocks,
+                            uint8_t* out, float* out_scale, hipStream_t stream);
+hipError_t launch_pack_mxfp4(const uint16_t* x, int64_t rows, int cols, int64_t x_stride,
+                             uint8_t* packed, int64_t packed_stride, uint8_t* scales,
+                             int64_t scale_stride, hipStream_t stream);
+hipError_t launch_plan(const int32_t* kv_indptr, int batch, int target_items, int max_items,
+                       int32_t* plan, hipStream_t stream);
+
+// decode.hip
+hipError_t launch_decode(const DecodeParams& p, int kv_mode, int grid, hipStream_t stream);
+hipError_t launch_combine(const DecodeParams& p, hipStream_t stream);
+
+// selftest.hip
+hipError_t launch_selftest(int which, const void* in, void* out, hipStream_t stream);
+
+}  // namespace mla

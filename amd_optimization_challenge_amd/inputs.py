@@ -1,0 +1,136 @@
+"""Seeded synthetic inputs in the reference's ``(q, kv_data, qo_indptr, kv_indptr, config)`` layout.
+
+Restates competitor_submissions/mi355x_reference/reference.py:288-346
+(``generate_input``) with two differences that make GPU and CPU runs see the
+same bits: random numbers come from a CPU ``torch.Generator`` (the reference
+draws on the GPU), and the caches are built on the device by this package's
+own bit-exact quantizers (``ops.quant_fp8_per_tensor``/``ops.pack_mxfp4``).
+
+Extensions over the reference (all optional keys, old callers unaffected):
+``config["num_heads"]`` (16 or 128), ``config["kv_indices"]`` (page-size-1
+slot per token), ``config["kv_mode"]`` (fp8 | mxfp4 | mxfp4k_fp8v) and a
+``config["sm_scale"]`` that is honoured.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+QK_DIM = 576
+V_DIM = 512
+
+# The five BASELINE configs.  sm_scale = 1/sqrt(192) throughout; lognormal
+# sigma for config 5 is fixed here at 1.0 (BASELINE leaves it open).
+CONFIGS = {
+    1: dict(name="cpu_plumbing", batch=4, num_heads=16, lens=("fixed", 256), kv_mode="fp8",
+            permute=False, seed=1001),
+    2: dict(name="tp_shard_b32_h16_l1024", batch=32, num_heads=16, lens=("fixed", 1024), kv_mode="fp8",
+            permute=True, seed=1002),
+    3: dict(name="h128_a8w8_b64_u512_8192", batch=64, num_heads=128, lens=("uniform", 512, 8192),
+            kv_mode="fp8", permute=True, seed=1003),
+    4: dict(name="mxfp4_b128_h16_l4096", batch=128, num_heads=16, lens=("fixed", 4096), kv_mode="mxfp4",
+            permute=True, seed=1004),
+    5: dict(name="mixed_b256_h128_lognormal1k", batch=256, num_heads=128,
+            lens=("lognormal", 1000.0, 1.0, 1, 32768), kv_mode="mxfp4k_fp8v", permute=True, seed=1005),
+}
+SM_SCALE = 1.0 / math.sqrt(192.0)
+
+
+def draw_lengths(spec, batch: int, gen: torch.Generator) -> torch.Tensor:
+    kind = spec[0]
+    if kind == "fixed":
+        return torch.full((batch,), int(spec[1]), dtype=torch.int64)
+    if kind == "uniform":  # integers in [lo, hi] inclusive
+        return torch.randint(int(spec[1]), int(spec[2]) + 1, (batch,), generator=gen, dtype=torch.int64)
+    if kind == "lognormal":  # round(exp(ln(median) + sigma * N(0,1))) clipped
+        _, median, sigma, lo, hi = spec
+        z = torch.randn((batch,), generator=gen, dtype=torch.float64)
+        L = torch.exp(math.log(median) + sigma * z).round().clamp(lo, hi)
+        return L.to(torch.int64)
+    if kind == "list":
+        return torch.as_tensor(spec[1], dtype=torch.int64)
+    raise ValueError(spec)
+
+
+def make_host_inputs(batch: int, num_heads: int, lens, seed: int, permute: bool = True):
+    """CPU tensors: q bf16 [B,H,576], kv bf16 [T,1,576], kv_indptr/kv_indices int32."""
+    gen = torch.Generator().manual_seed(int(seed))
+    L = draw_lengths(lens, batch, gen) if not torch.is_tensor(lens) else lens.to(torch.int64)
+    q = torch.randn((batch, num_heads, QK_DIM), generator=gen, dtype=torch.bfloat16)
+    T = int(L.sum())
+    kv = torch.randn((max(T, 1), 1, QK_DIM), generator=gen, dtype=torch.bfloat16)
+    if permute:
+        kv_indices = torch.randperm(T, generator=gen).to(torch.int32)
+    else:
+        kv_indices = torch.arange(T, dtype=torch.int32)
+    kv_indptr = torch.zeros(batch + 1, dtype=torch.int32)
+    kv_indptr[1:] = torch.cumsum(L, 0).to(torch.int32)
+    return q, kv, kv_indptr, kv_indices
+
+
+def build_kv_data(kv: torch.Tensor, kv_mode: str) -> dict:
+    """Device caches from a device bf16 [T,1,576] cache with this package's quantizers."""
+    from . import ops
+
+    kv_data = {"bf16": kv}
+    if kv_mode in ("fp8", "mxfp4k_fp8v"):
+        fp8, sc = ops.quant_fp8_per_tensor(kv)
+        kv_data["fp8"] = (fp8, sc)
+    if kv_mode in ("mxfp4", "mxfp4k_fp8v"):
+        packed, scales = ops.pack_mxfp4(kv.reshape(-1, QK_DIM))
+        kv_data["mxfp4"] = (packed.view(torch.float4_e2m1fn_x2).reshape(kv.shape[0], 1, QK_DIM // 2),
+                            scales.view(torch.float8_e8m0fnu))
+    return kv_data
+
+
+def make_config(batch, num_heads, kv_lens_total, kv_mode, sm_scale, kv_indices, kv_seq_len):
+    return {
+        "batch_size": batch,
+        "num_heads": num_heads,
+        "num_kv_heads": 1,
+        "qk_head_dim": QK_DIM,
+        "kv_lora_rank": V_DIM,
+        "qk_rope_head_dim": QK_DIM - V_DIM,
+        "v_head_dim": V_DIM,
+        "q_seq_len": 1,
+        "kv_seq_len": kv_seq_len,
+        "sm_scale": sm_scale,
+        "kv_mode": kv_mode,
+        "kv_indices": kv_indices,
+        "total_kv": kv_lens_total,
+    }
+
+
+def generate_config(cid: int, device="cuda", seed: int | None = None):
+    """Inputs of BASELINE config ``cid`` on ``device`` (caches built there)."""
+    spec = CONFIGS[cid]
+    seed = spec["seed"] if seed is None else seed
+    return generate(spec["batch"], spec["num_heads"], spec["lens"], spec["kv_mode"], seed,
+                    permute=spec["permute"], sm_scale=SM_SCALE, device=device)
+
+
+def generate(batch, num_heads, lens, kv_mode, seed, permute=True, sm_scale=SM_SCALE, device="cuda"):
+    q, kv, kv_indptr, kv_indices = make_host_inputs(batch, num_heads, lens, seed, permute)
+    dev = torch.device(device)
+    q_d, kv_d = q.to(dev), kv.to(dev)
+    kv_data = build_kv_data(kv_d, kv_mode)
+    indptr_d, indices_d = kv_indptr.to(dev), kv_indices.to(dev)
+    lens_t = (kv_indptr[1:] - kv_indptr[:-1])
+    max_len = int(lens_t.max()) if batch else 0
+    qo_indptr = torch.arange(batch + 1, dtype=torch.int32, device=dev)
+    cfg = make_config(batch, num_heads, int(kv_indptr[-1]), kv_mode, sm_scale, indices_d, max_len)
+    return (q_d, kv_data, qo_indptr, indptr_d, cfg)
+
+
+def generate_input(batchsize: int, qseqlen: int, kvseqlen: int, seed: int, device="cuda"):
+    """Reference-signature generator (reference.py:288): H = 16, uniform lengths,
+    contiguous cache (kv_indices = arange), sm_scale = 1/sqrt(576), fp8 route."""
+    if qseqlen != 1:
+        raise NotImplementedError("decode only: qseqlen must be 1")
+    data = generate(batchsize, 16, ("fixed", kvseqlen), "fp8", seed, permute=False,
+                    sm_scale=1.0 / math.sqrt(QK_DIM), device=device)
+    q, kv_data, qo, kv_indptr, cfg = data
+    kv_data.update(build_kv_data(kv_data["bf16"], "mxfp4"))
+    cfg["kv_indices"] = None
+    return (q, kv_data, qo, kv_indptr, cfg)

@@ -1,0 +1,209 @@
+"""torch-facing wrappers of the C ABI.  PyTorch supplies device memory and the
+current HIP stream; every computation runs in libmla_mi355x.so.
+
+All functions take device tensors and enqueue work on
+``torch.cuda.current_stream()``; none synchronizes the host.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+
+QK_DIM = 576
+V_DIM = 512
+FP4_ROW = 288
+MX_BLOCKS = 18
+
+
+def _stream() -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _ptr(t) -> ctypes.c_void_p:
+    return ctypes.c_void_p(0 if t is None else t.data_ptr())
+
+
+def _require_cuda(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise ValueError("tensors must live on a HIP device")
+
+
+def kv_mode_id(kv_mode) -> int:
+    if isinstance(kv_mode, int):
+        return kv_mode
+    try:
+        return _lib.KV_MODES[kv_mode]
+    except KeyError:
+        raise ValueError(f"unknown kv_mode {kv_mode!r}; expected one of {sorted(_lib.KV_MODES)}")
+
+
+def as_bytes(t: torch.Tensor) -> torch.Tensor:
+    """Reinterpret a 1-byte-element tensor (fp8 / fp4x2 / e8m0 / uint8) as uint8."""
+    if t.element_size() != 1:
+        raise ValueError(f"expected a 1-byte dtype, got {t.dtype}")
+    return t if t.dtype == torch.uint8 else t.view(torch.uint8)
+
+
+def cu_count() -> int:
+    n = ctypes.c_int(0)
+    _lib.check(_lib.load().mla_device_cu_count(ctypes.byref(n)), "mla_device_cu_count")
+    return n.value
+
+
+def workspace_bytes(batch: int, num_heads: int, kv_mode) -> int:
+    n = ctypes.c_int64(0)
+    _lib.check(_lib.load().mla_workspace_bytes(batch, num_heads, kv_mode_id(kv_mode), ctypes.byref(n)),
+               "mla_workspace_bytes")
+    return n.value
+
+
+_ws_cache: dict = {}
+
+
+def workspace(batch: int, num_heads: int, kv_mode, device) -> torch.Tensor:
+    """Workspace for a shape, cached per (shape, device) -- keyed on shapes only."""
+    device = torch.device(device)
+    key = (batch, num_heads, kv_mode_id(kv_mode), device)
+    ws = _ws_cache.get(key)
+    if ws is None:
+        with torch.cuda.device(device):
+            ws = torch.empty(workspace_bytes(batch, num_heads, kv_mode), dtype=torch.uint8, device=device)
+        _ws_cache[key] = ws
+    return ws
+
+
+# ---------------------------------------------------------------------------
+# quantizers (bit exact to the reference's; see oracle/mla_oracle.py)
+# ---------------------------------------------------------------------------
+
+
+def quant_fp8_per_tensor(x: torch.Tensor, out: torch.Tensor | None = None,
+                         scale: torch.Tensor | None = None):
+    """bf16 tensor -> (float8_e4m3fn tensor of the same shape, f32 scale [1]).
+
+    competitor_submissions/mi355x_reference/reference.py:65-80 (quantize_fp8).
+    """
+    _require_cuda(x)
+    if x.dtype != torch.bfloat16:
+        raise ValueError("x must be bfloat16")
+    x = x.contiguous()
+    if out is None:
+        out = torch.empty(x.shape, dtype=torch.float8_e4m3fn, device=x.device)
+    if scale is None:
+        scale = torch.empty(1, dtype=torch.float32, device=x.device)
+    scratch = torch.empty(8192, dtype=torch.uint8, device=x.device)
+    with torch.cuda.device(x.device):
+        _lib.check(_lib.load().mla_quant_fp8_per_tensor(_ptr(x), x.numel(), _ptr(out), _ptr(scale),
+                                                        _ptr(scratch), scratch.numel(), _stream()),
+                   "mla_quant_fp8_per_tensor")
+    return out, scale
+
+
+def pack_mxfp4(x: torch.Tensor, scale_cols: int | None = None):
+    """bf16 [..., cols] -> (packed uint8 [..., cols/2], e8m0 uint8 [rows, scale_cols]).
+
+    competitor_submissions/mi355x_reference/reference.py:88-113 (quantize_mxfp4).
+    ``scale_cols`` (>= cols/32) pads the scale rows like AITER may; padding
+    bytes are left as 127 (2^0).
+    """
+    _require_cuda(x)
+    if x.dtype != torch.bfloat16:
+        raise ValueError("x must be bfloat16")
+    cols = x.shape[-1]
+    if cols % 32:
+        raise ValueError("last dim must be a multiple of 32")
+    x2 = x.reshape(-1, cols).contiguous()
+    rows = x2.shape[0]
+    nsc = cols // 32 if scale_cols is None else int(scale_cols)
+    if nsc < cols // 32:
+        raise ValueError("scale_cols < cols/32")
+    packed = torch.empty((rows, cols // 2), dtype=torch.uint8, device=x.device)
+    scales = torch.full((rows, nsc), 127, dtype=torch.uint8, device=x.device)
+    with torch.cuda.device(x.device):
+        _lib.check(_lib.load().mla_pack_mxfp4(_ptr(x2), rows, cols, x2.stride(0) * 2, _ptr(packed),
+                                              packed.stride(0), _ptr(scales), scales.stride(0), _stream()),
+                   "mla_pack_mxfp4")
+    return packed.reshape(*x.shape[:-1], cols // 2), scales
+
+
+# ---------------------------------------------------------------------------
+# decode pipeline stages
+# ---------------------------------------------------------------------------
+
+
+def _kv_args(kv_mode: int, kv_data: dict):
+    """(k_cache, k_row_stride, k_scales, k_scale_stride, v_cache, v_row_stride, kv_scale)."""
+    if kv_mode == 0:
+        fp8, sc = kv_data["fp8"]
+        k = as_bytes(fp8).reshape(fp8.shape[0], -1)
+        return k, k.stride(0), None, 0, None, 0, sc
+    if kv_mode == 1:
+        fp4, e8 = kv_data["mxfp4"]
+        k = as_bytes(fp4).reshape(fp4.shape[0], -1)
+        s = as_bytes(e8)
+        return k, k.stride(0), s, s.stride(0), None, 0, None
+    if kv_mode == 2:
+        fp4, e8 = kv_data["mxfp4"]
+        fp8, sc = kv_data["fp8"]
+        k = as_bytes(fp4).reshape(fp4.shape[0], -1)
+        s = as_bytes(e8)
+        v = as_bytes(fp8).reshape(fp8.shape[0], -1)
+        return k, k.stride(0), s, s.stride(0), v, v.stride(0), sc
+    raise ValueError(kv_mode)
+
+
+def plan(kv_indptr: torch.Tensor, batch: int, num_heads: int, kv_mode, ws: torch.Tensor) -> None:
+    with torch.cuda.device(ws.device):
+        _lib.check(_lib.load().mla_plan(_ptr(kv_indptr), batch, num_heads, kv_mode_id(kv_mode), _ptr(ws),
+                                        ws.numel(), _stream()), "mla_plan")
+
+
+def decode(q_fp8, q_scale, kv_data, kv_indptr, kv_indices, num_heads, sm_scale, kv_mode, ws, out):
+    mode = kv_mode_id(kv_mode)
+    k, ks, ksc, kss, v, vs, sc = _kv_args(mode, kv_data)
+    batch = kv_indptr.numel() - 1
+    with torch.cuda.device(ws.device):
+        _lib.check(_lib.load().mla_decode(
+            _ptr(q_fp8), _ptr(q_scale), _ptr(k), ks, _ptr(ksc), kss, _ptr(v), vs, _ptr(sc),
+            _ptr(kv_indptr), _ptr(kv_indices), batch, num_heads, float(sm_scale), mode, _ptr(ws),
+            ws.numel(), _ptr(out), _stream()), "mla_decode")
+
+
+def combine(batch: int, num_heads: int, ws: torch.Tensor, out: torch.Tensor) -> None:
+    with torch.cuda.device(ws.device):
+        _lib.check(_lib.load().mla_combine(batch, num_heads, _ptr(ws), ws.numel(), _ptr(out), _stream()),
+                   "mla_combine")
+
+
+def decode_fwd(q, kv_data, kv_indptr, kv_indices, sm_scale, kv_mode="fp8", out=None, ws=None):
+    """Whole operator: FP8-quantize q, plan, decode, combine.  q: bf16 [B, H, 576]."""
+    _require_cuda(q, kv_indptr, kv_indices)
+    if q.dtype != torch.bfloat16 or q.dim() != 3 or q.shape[-1] != QK_DIM:
+        raise ValueError("q must be bf16 [batch, heads, 576]")
+    if kv_indptr.dtype != torch.int32 or (kv_indices is not None and kv_indices.dtype != torch.int32):
+        raise ValueError("kv_indptr / kv_indices must be int32")
+    q = q.contiguous()
+    batch, num_heads = q.shape[0], q.shape[1]
+    if kv_indptr.numel() != batch + 1:
+        raise ValueError(f"kv_indptr has {kv_indptr.numel()} entries, expected batch+1 = {batch + 1}")
+    mode = kv_mode_id(kv_mode)
+    k, ks, ksc, kss, v, vs, sc = _kv_args(mode, kv_data)
+    if ws is None:
+        ws = workspace(batch, num_heads, mode, q.device)
+    if out is None:
+        out = torch.empty((batch, num_heads, V_DIM), dtype=torch.bfloat16, device=q.device)
+    with torch.cuda.device(q.device):
+        _lib.check(_lib.load().mla_decode_fwd(
+            _ptr(q), _ptr(k), ks, _ptr(ksc), kss, _ptr(v), vs, _ptr(sc), _ptr(kv_indptr),
+            _ptr(kv_indices), batch, num_heads, float(sm_scale), mode, _ptr(ws), ws.numel(), _ptr(out),
+            _stream()), "mla_decode_fwd")
+    return out
+
+
+def selftest(which: int, inp: torch.Tensor, out: torch.Tensor) -> None:
+    with torch.cuda.device(inp.device):
+        _lib.check(_lib.load().mla_selftest(which, _ptr(inp), _ptr(out), _stream()), "mla_selftest")

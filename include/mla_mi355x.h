@@ -1,0 +1,142 @@
+/*
+ * mla_mi355x.h -- C ABI of the MI355X (gfx950) MLA absorbed-decode operator.
+ *
+ * Every entry point is `extern "C"`, takes plain device pointers, sizes and a
+ * HIP stream handle (`void*`, 0 = the null stream), never synchronizes the
+ * host, never allocates device memory, and returns an `int` status
+ * (MLA_OK = 0).  On failure `mla_last_error()` returns a message for the
+ * calling thread.  All device memory is caller-owned; scratch lives in the
+ * caller-provided workspace whose size `mla_workspace_bytes` reports.
+ *
+ * Layouts (row-major, byte strides given in bytes):
+ *   q            [batch, num_heads, 576]  bf16          (q_seq_len = 1)
+ *   q_fp8        [batch, num_heads, 576]  float8 e4m3fn (OCP)
+ *   fp8 cache    [slots, 576]             e4m3fn, one per-tensor f32 scale
+ *   mxfp4 cache  [slots, 288]             e2m1 pairs, low nibble = even element
+ *   mxfp4 scales [slots, scale_stride]    e8m0, first 18 used (stride >= 18)
+ *   kv_indptr    [batch + 1]              int32, token offsets into kv_indices
+ *   kv_indices   [kv_indptr[batch]]       int32 cache slot per token (page size 1);
+ *                                         NULL means identity (slot = offset)
+ *   out          [batch, num_heads, 512]  bf16
+ *
+ * References below are path:line in dorhuri123/AMD_optimization_challenge.
+ */
+#ifndef MLA_MI355X_H
+#define MLA_MI355X_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* status codes */
+#define MLA_OK 0
+#define MLA_ERR_INVALID_ARGUMENT 1
+#define MLA_ERR_UNSUPPORTED 2
+#define MLA_ERR_WORKSPACE_TOO_SMALL 3
+#define MLA_ERR_HIP 4
+
+/* kv_mode: which cache feeds the scores (K, 576 dims) and the values (V, 512 dims) */
+#define MLA_KV_FP8 0          /* K = V = fp8 cache (V = first 512 dims)            */
+#define MLA_KV_MXFP4 1        /* K = V = mxfp4 cache (V = first 256 B + 16 scales)   */
+#define MLA_KV_MXFP4K_FP8V 2  /* K = mxfp4 cache, V = first 512 dims of fp8 cache    */
+
+/* Message describing the last failure on this thread ("" if none). */
+const char* mla_last_error(void);
+
+/* ABI version, bumped on any signature change. */
+int mla_abi_version(void);
+
+/* Number of compute units on the current device (used by the split planner). */
+int mla_device_cu_count(int* num_cu);
+
+/*
+ * Workspace size for one decode call of this shape.  Replaces the buffer sizing
+ * of AITER's get_mla_metadata_info_v1 (competitor_submissions/mi355x_reference/
+ * reference.py:174-179) plus the logits/lse allocations of mla_decode_fwd
+ * (mixed-mla/asm_dumps/aiter_mla.py:357-366).
+ */
+int mla_workspace_bytes(int batch, int num_heads, int kv_mode, int64_t* bytes);
+
+/*
+ * Per-tensor FP8 quantization of n bf16 values: amax -> scale = bf16(amax/448)
+ * -> e4m3fn(clamp(bf16(x/scale), +-448)), bit-exact to quantize_fp8
+ * (competitor_submissions/mi355x_reference/reference.py:65-80).  Writes the f32
+ * scale to out_scale[0].  workspace needs >= 8 KiB; it is left reusable.
+ */
+int mla_quant_fp8_per_tensor(const void* x_bf16, int64_t n, void* out_fp8,
+                             float* out_scale, void* workspace,
+                             int64_t workspace_bytes, void* stream);
+
+/*
+ * MXFP4 pack of `rows` bf16 rows of `cols` elements (cols % 32 == 0): one e8m0
+ * per 32 elements plus e2m1 nibbles, bit-exact to quantize_mxfp4 /
+ * dynamic_mxfp4_quant (competitor_submissions/mi355x_reference/reference.py:88-113,
+ * algorithm restated at mxfp4-mm/submission_v18_custom_fused.py:26-108).
+ * Strides in bytes.  Scale columns beyond cols/32 are not written.
+ */
+int mla_pack_mxfp4(const void* x_bf16, int64_t rows, int cols, int64_t x_row_stride,
+                   void* packed, int64_t packed_row_stride, void* scales,
+                   int64_t scale_row_stride, void* stream);
+
+/*
+ * Split-KV work partition, computed on the device from kv_indptr (no host
+ * sync).  Replaces get_mla_metadata_v1
+ * (competitor_submissions/mi355x_reference/reference.py:161-209) and the
+ * uniform cdiv split of mixed-mla/submission.py:158-160.  The plan lives in the
+ * workspace and is consumed by mla_decode / mla_combine.
+ */
+int mla_plan(const int32_t* kv_indptr, int batch, int num_heads, int kv_mode,
+             void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Split-KV decode over a plan made by mla_plan: per work item, QK^T over the
+ * 576-d latent and PV over the 512-d latent with an online softmax; finished
+ * sequences are written to `out`, split ones to workspace partials.  Replaces
+ * mla_decode_stage1_asm_fwd (mixed-mla/asm_dumps/aiter_mla.py:398-419).
+ *   fp8 K   : k_cache = fp8 cache, k_row_stride >= 576, k_scales unused
+ *   mxfp4 K : k_cache = packed cache (row stride >= 288), k_scales = e8m0
+ *   fp8 V   : v_cache = fp8 cache (row stride >= 512), kv_scale = its scale
+ *   mxfp4 V : same rows as K (v_cache ignored)
+ * Scores are (q_fp8*q_scale).(k*k_scale) * sm_scale.
+ */
+int mla_decode(const void* q_fp8, const float* q_scale, const void* k_cache,
+               int64_t k_row_stride, const void* k_scales, int64_t k_scale_stride,
+               const void* v_cache, int64_t v_row_stride, const float* kv_scale,
+               const int32_t* kv_indptr, const int32_t* kv_indices, int batch,
+               int num_heads, float sm_scale, int kv_mode, void* workspace,
+               int64_t workspace_bytes, void* out_bf16, void* stream);
+
+/*
+ * Log-sum-exp merge of the split partials of every split sequence into `out`
+ * (bf16).  Replaces mla_reduce_v1 (mixed-mla/asm_dumps/aiter_mla.py:421-430).
+ */
+int mla_combine(int batch, int num_heads, void* workspace, int64_t workspace_bytes,
+                void* out_bf16, void* stream);
+
+/*
+ * The whole operator: quantize q (bf16) to FP8, plan, decode, combine.  This is
+ * the C side of custom_kernel(data) (mixed-mla/submission.py:626-644) for
+ * q_seq_len = 1; the per-step entry points above are its stages.
+ */
+int mla_decode_fwd(const void* q_bf16, const void* k_cache, int64_t k_row_stride,
+                   const void* k_scales, int64_t k_scale_stride, const void* v_cache,
+                   int64_t v_row_stride, const float* kv_scale,
+                   const int32_t* kv_indptr, const int32_t* kv_indices, int batch,
+                   int num_heads, float sm_scale, int kv_mode, void* workspace,
+                   int64_t workspace_bytes, void* out_bf16, void* stream);
+
+/*
+ * Diagnostics (no counterpart in the reference): runs one wave of a built-in
+ * check that pins an MFMA operand/accumulator layout or a conversion the
+ * kernels rely on.  `in`/`out` are small device buffers whose layout per
+ * `which` is documented in csrc/selftest.hip.
+ */
+int mla_selftest(int which, const void* in, void* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MLA_MI355X_H */

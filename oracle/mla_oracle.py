@@ -1,0 +1,381 @@
+"""CPU oracle for the MLA absorbed-decode hot path.
+
+TEST INFRASTRUCTURE ONLY.  Only ``tests/``, ``__graft_entry__.smoke()`` and the
+``cpu_baseline`` leg of ``bench.py`` may import this module, and only as the
+checker (or as the timed CPU baseline).  The product path never routes through
+it: ``amd_optimization_challenge_amd`` raises if its HIP library is missing.
+
+What it restates (all citations relative to the reference checkout):
+
+* ``quantize_fp8_per_tensor``  -- TASK/reference.py:65-80 (``quantize_fp8``),
+  with torch's bf16 arithmetic made explicit: |x| max in bf16, clamp(min=1e-12)
+  in bf16, ``amax / 448`` rounded to bf16, ``x / scale`` rounded to bf16,
+  clamp to +-448, round-to-nearest-even cast to float8_e4m3fn.
+* ``pack_mxfp4``               -- TASK/reference.py:88-113 -> AITER
+  ``dynamic_mxfp4_quant``, whose algorithm the reference restates at
+  mxfp4-mm/submission_v18_custom_fused.py:26-108 (``_mxfp4_quant_op``).
+  AITER itself is not vendored (un-pinned HEAD clone, setup.sh:52-61), so the
+  restatement there is the anchor.
+* ``dequant_fp8`` / ``dequant_mxfp4`` -- TASK/reference.py:73-74 and
+  TASK/reference.py:116-154; e2m1 table from mixed-mla/triton_mla_mxfp4.py:21-31,
+  e8m0 = 2^(e-127) from mixed-mla/triton_mla_mxfp4.py:59.
+* ``mla_decode``               -- the dequantize-then-fp32
+  softmax(Q K^T * sm_scale) V that ``ref_kernel`` (TASK/reference.py:349-369)
+  approximates through AITER, gathered through ``kv_indices`` (page size 1).
+
+Independence from the kernels: the element encoders here are *table searches*
+(nearest representable value, ties to the even code), not the bit tricks the
+HIP kernels and the reference use, so agreement between the two is evidence.
+
+Parity pins (see tests/test_oracle_*.py):
+  fp8 quant   -- exhaustive against torch's own float8_e4m3fn cast (the
+                 third-party routine the reference calls), plus closed-form
+                 invariants.
+  mxfp4 pack  -- exhaustive element encoding against the reference's bit-trick
+                 formula (restated in the test), scale-rule known answers,
+                 round trip.
+  attention   -- float64 brute force on tiny shapes, closed forms (kv_len=1,
+                 identical keys), permutation/split invariance.
+"""
+from __future__ import annotations
+
+import math
+import os
+import time
+
+import numpy as np
+
+QK_DIM = 576
+V_DIM = 512
+MX_BLOCK = 32
+FP8_MAX = 448.0
+BF16_1E_12 = 0x2B8D  # torch: tensor(0., bf16).clamp(min=1e-12) -> bits 0x2b8d
+
+# ----------------------------------------------------------------------------
+# bf16 <-> f32
+# ----------------------------------------------------------------------------
+
+
+def bf16_to_f32(bits: np.ndarray) -> np.ndarray:
+    """bf16 bit patterns (uint16) -> float32 values (exact)."""
+    return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16(x: np.ndarray) -> np.ndarray:
+    """float32 -> bf16 bits, round to nearest, ties to even (finite inputs).
+
+    Written as a neighbour comparison: the two bf16 candidates are the
+    truncation and the next value up; pick the closer, ties to the one whose
+    last mantissa bit is 0.
+    """
+    x = np.asarray(x, dtype=np.float32)
+    u = x.view(np.uint32)
+    lo = (u >> 16).astype(np.uint32)
+    hi = lo + 1
+    vlo = (lo << 16).view(np.float32).astype(np.float64)
+    vhi = (hi << 16).view(np.float32).astype(np.float64)
+    xd = x.astype(np.float64)
+    dlo = np.abs(xd - vlo)
+    dhi = np.abs(vhi - xd)
+    pick_hi = (dhi < dlo) | ((dhi == dlo) & ((lo & 1) == 1))
+    out = np.where(pick_hi, hi, lo)
+    return out.astype(np.uint16)
+
+
+# ----------------------------------------------------------------------------
+# float8 e4m3fn (OCP) -- decode table and RNE encode by table search
+# ----------------------------------------------------------------------------
+
+
+def _e4m3fn_table() -> np.ndarray:
+    vals = np.zeros(256, dtype=np.float64)
+    for c in range(256):
+        s = -1.0 if c & 0x80 else 1.0
+        e = (c >> 3) & 0xF
+        m = c & 0x7
+        if e == 0xF and m == 0x7:
+            vals[c] = np.nan
+        elif e == 0:
+            vals[c] = s * (m / 8.0) * 2.0 ** -6
+        else:
+            vals[c] = s * (1.0 + m / 8.0) * 2.0 ** (e - 7)
+    return vals
+
+
+E4M3FN = _e4m3fn_table()
+_E4M3_POS = E4M3FN[:127]  # codes 0x00..0x7E, monotone increasing 0..448
+
+
+def e4m3fn_to_f32(codes: np.ndarray) -> np.ndarray:
+    return E4M3FN[np.asarray(codes, dtype=np.uint8)].astype(np.float32)
+
+
+def f32_to_e4m3fn(x: np.ndarray) -> np.ndarray:
+    """float32 -> e4m3fn code, nearest value, ties to even code; |x| > 448 saturates.
+
+    Callers clamp to +-448 first (TASK/reference.py:79), so saturation is never
+    reached on the reference path.
+    """
+    x = np.asarray(x, dtype=np.float64)
+    a = np.minimum(np.abs(x), FP8_MAX)
+    hi = np.searchsorted(_E4M3_POS, a, side="left")  # first value >= a
+    hi = np.minimum(hi, 126)
+    lo = np.maximum(hi - 1, 0)
+    vlo = _E4M3_POS[lo]
+    vhi = _E4M3_POS[hi]
+    dlo = a - vlo
+    dhi = vhi - a
+    exact = vhi == a
+    pick_hi = exact | (dhi < dlo) | ((dhi == dlo) & (hi % 2 == 0))
+    code = np.where(pick_hi, hi, lo).astype(np.uint8)
+    sign = (np.signbit(x)).astype(np.uint8) << 7
+    return code | sign
+
+
+# ----------------------------------------------------------------------------
+# a2: per-tensor FP8 quantization (TASK/reference.py:65-80)
+# ----------------------------------------------------------------------------
+
+
+def fp8_scale_from_amax_bits(amax_bits: int) -> tuple[int, float]:
+    """bf16 amax bits -> (bf16 scale bits, f32 scale) as torch computes it.
+
+    TASK/reference.py:77-78: ``amax.clamp(min=1e-12)`` then ``amax / finfo.max``,
+    both in bf16.  The division result is rounded to bf16.
+    """
+    amax_bits = max(int(amax_bits), BF16_1E_12) if amax_bits <= 0x7F80 else int(amax_bits)
+    a = float(bf16_to_f32(np.array([amax_bits], dtype=np.uint16))[0])
+    s_bits = int(f32_to_bf16(np.array([np.float32(a) / np.float32(FP8_MAX)], dtype=np.float32))[0])
+    return s_bits, float(bf16_to_f32(np.array([s_bits], dtype=np.uint16))[0])
+
+
+def quantize_fp8_per_tensor(x_bits: np.ndarray) -> tuple[np.ndarray, float]:
+    """bf16 bits (any shape) -> (e4m3fn codes, same shape; float32 scale).
+
+    Restates TASK/reference.py:76-80 step by step:
+      amax   = bf16 max|x|                      (exact)
+      amax   = max(amax, bf16(1e-12))           (clamp in bf16)
+      scale  = bf16(amax / 448)
+      y      = bf16(x / scale)                  (f32 divide, RNE to bf16)
+      y      = clamp(y, -448, 448)
+      codes  = e4m3fn_rne(y)
+      return codes, float32(scale)
+    """
+    bits = np.asarray(x_bits, dtype=np.uint16)
+    mag = (bits & 0x7FFF).astype(np.uint32)
+    amax_bits = int(mag.max()) if mag.size else 0
+    s_bits, scale = fp8_scale_from_amax_bits(amax_bits)
+    xf = bf16_to_f32(bits)
+    y_bits = f32_to_bf16(xf / np.float32(scale))
+    y = bf16_to_f32(y_bits)
+    y = np.clip(y, -FP8_MAX, FP8_MAX)
+    return f32_to_e4m3fn(y), np.float32(scale)
+
+
+def dequant_fp8(codes: np.ndarray, scale: float) -> np.ndarray:
+    """TASK/reference.py:73-74 (``fp8.to(bf16) * scale``), computed in float32."""
+    return e4m3fn_to_f32(codes) * np.float32(scale)
+
+
+# ----------------------------------------------------------------------------
+# a4: MXFP4 (e2m1 values, e8m0 scale per 32 elements)
+# ----------------------------------------------------------------------------
+
+E2M1 = np.array([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0], dtype=np.float64)
+
+
+def mxfp4_block_scale(amax: np.ndarray) -> np.ndarray:
+    """Per-block e8m0 byte from the block's float32 |x| max.
+
+    mxfp4-mm/submission_v18_custom_fused.py:50-57: round amax up to the next
+    power of two when its mantissa is >= 1.75 (add 2^21 to the f32 bits, drop
+    the mantissa), take floor(log2) - 2, clamp to [-127, 127], bias by 127.
+    A block of zeros gives 0.  A round-up that overflows the exponent gives
+    +inf, whose clamp is 127 (byte 254).
+    """
+    a = np.asarray(amax, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    r = ((a + 0x200000) & 0xFF800000).astype(np.uint64)
+    expf = (r >> 23) & 0xFF
+    # floor(log2(r)): r is a power of two (or 0 / denormal-free after the mask)
+    unb = np.where(r == 0, -1000, expf.astype(np.int64) - 127)
+    unb = np.where(expf == 0xFF, 1000, unb)  # +inf
+    e = np.clip(unb - 2, -127, 127)
+    return (e + 127).astype(np.uint8)
+
+
+def f32_to_e2m1(q: np.ndarray) -> np.ndarray:
+    """float -> e2m1 nibble: nearest grid value, ties to the even code, >= 6 -> 7.
+
+    Sign in bit 3 (mxfp4-mm/submission_v18_custom_fused.py:96-98); -0 keeps it.
+    """
+    q = np.asarray(q, dtype=np.float64)
+    a = np.abs(q)
+    hi = np.searchsorted(E2M1, a, side="left")
+    hi = np.minimum(hi, 7)
+    lo = np.maximum(hi - 1, 0)
+    dlo = a - E2M1[lo]
+    dhi = E2M1[hi] - a
+    exact = E2M1[hi] == a
+    pick_hi = exact | (dhi < dlo) | ((dhi == dlo) & (hi % 2 == 0))
+    code = np.where(pick_hi, hi, lo)
+    code = np.where(a >= 6.0, 7, code).astype(np.uint8)
+    sign = np.signbit(q).astype(np.uint8) << 3
+    return code | sign
+
+
+def pack_mxfp4(x_bits: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """bf16 bits [rows, cols] -> (packed uint8 [rows, cols/2], e8m0 uint8 [rows, cols/32]).
+
+    Pack order: low nibble = even element (TASK/README.md:78;
+    mxfp4-mm/submission_v18_custom_fused.py:100-106).
+    """
+    bits = np.asarray(x_bits, dtype=np.uint16)
+    rows, cols = bits.shape
+    assert cols % MX_BLOCK == 0
+    x = bf16_to_f32(bits).reshape(rows, cols // MX_BLOCK, MX_BLOCK)
+    amax = np.abs(x).max(axis=-1)
+    e8 = mxfp4_block_scale(amax)
+    unb = e8.astype(np.int64) - 127
+    q = x.astype(np.float64) * np.exp2(-unb.astype(np.float64))[..., None]
+    q = q.astype(np.float32)  # x * 2^-e is exact in f32 for every finite bf16 block
+    codes = f32_to_e2m1(q).reshape(rows, cols)
+    packed = (codes[:, 0::2] | (codes[:, 1::2] << 4)).astype(np.uint8)
+    return packed, e8
+
+
+def dequant_mxfp4(packed: np.ndarray, scales: np.ndarray, cols: int) -> np.ndarray:
+    """TASK/reference.py:116-154: e2m1 value * 2^(e8m0-127), float32.
+
+    ``scales`` may carry padding columns (TASK/reference.py:146-148); only the
+    first cols/32 are used.
+    """
+    packed = np.asarray(packed, dtype=np.uint8)
+    rows = packed.shape[0]
+    lo = packed & 0xF
+    hi = packed >> 4
+    codes = np.empty((rows, cols), dtype=np.uint8)
+    codes[:, 0::2] = lo[:, : cols // 2]
+    codes[:, 1::2] = hi[:, : cols // 2]
+    mag = E2M1[codes & 7]
+    val = np.where(codes & 8, -mag, mag)
+    sc = np.exp2(np.asarray(scales[:, : cols // MX_BLOCK], dtype=np.float64) - 127.0)
+    val = val.reshape(rows, cols // MX_BLOCK, MX_BLOCK) * sc[..., None]
+    return val.reshape(rows, cols).astype(np.float32)
+
+
+# ----------------------------------------------------------------------------
+# a7/a8: attention over the dequantized cache
+# ----------------------------------------------------------------------------
+
+
+def dequant_kv(kv_mode: str, fp8_codes=None, fp8_scale=None, fp4_packed=None,
+               fp4_scales=None) -> tuple[np.ndarray, np.ndarray]:
+    """Return (K [T,576] f32, V [T,512] f32) for a kv_mode.
+
+    fp8          : K = V-source = fp8 cache (V = first 512 dims)
+    mxfp4        : K = mxfp4 cache, V = first 512 dims of the same cache
+    mxfp4k_fp8v  : K = mxfp4 cache (576), V = fp8 cache (first 512 dims)
+    """
+    if kv_mode == "fp8":
+        k = dequant_fp8(fp8_codes.reshape(-1, QK_DIM), fp8_scale)
+        return k, k[:, :V_DIM]
+    if kv_mode == "mxfp4":
+        k = dequant_mxfp4(fp4_packed.reshape(-1, QK_DIM // 2), fp4_scales, QK_DIM)
+        return k, k[:, :V_DIM]
+    if kv_mode == "mxfp4k_fp8v":
+        k = dequant_mxfp4(fp4_packed.reshape(-1, QK_DIM // 2), fp4_scales, QK_DIM)
+        v = dequant_fp8(fp8_codes.reshape(-1, QK_DIM), fp8_scale)[:, :V_DIM]
+        return k, v
+    raise ValueError(kv_mode)
+
+
+def mla_decode(q_deq, k_deq, v_deq, kv_indptr, kv_indices, sm_scale, threads=None):
+    """out[b,h,:] = softmax(q[b,h] . K[idx_b]^T * sm_scale) V[idx_b], float32.
+
+    q_deq [B,H,576] f32; k_deq [T,576]; v_deq [T,512]; kv_indices maps each
+    logical token to a cache row (page size 1).  An empty sequence yields 0.
+    Computed with torch on the CPU (batched fp32 GEMM), one sequence at a time.
+    """
+    import torch
+
+    if threads:
+        torch.set_num_threads(threads)
+    q = torch.as_tensor(np.ascontiguousarray(q_deq), dtype=torch.float32)
+    k = torch.as_tensor(np.ascontiguousarray(k_deq), dtype=torch.float32)
+    v = torch.as_tensor(np.ascontiguousarray(v_deq), dtype=torch.float32)
+    indptr = np.asarray(kv_indptr, dtype=np.int64)
+    idx = torch.as_tensor(np.asarray(kv_indices, dtype=np.int64))
+    B, H, _ = q.shape
+    out = torch.zeros((B, H, V_DIM), dtype=torch.float32)
+    for b in range(B):
+        s0, s1 = int(indptr[b]), int(indptr[b + 1])
+        if s1 <= s0:
+            continue
+        rows = idx[s0:s1]
+        kb = k.index_select(0, rows)
+        vb = v.index_select(0, rows)
+        s = (q[b] @ kb.T) * float(sm_scale)
+        p = torch.softmax(s, dim=-1)
+        out[b] = p @ vb
+    return out.numpy()
+
+
+def mla_decode_f64(q_deq, k_deq, v_deq, kv_indptr, kv_indices, sm_scale):
+    """Float64 pure-numpy brute force (small shapes only), explicit max-shifted softmax."""
+    q = np.asarray(q_deq, np.float64)
+    B, H, _ = q.shape
+    out = np.zeros((B, H, V_DIM), np.float64)
+    for b in range(B):
+        s0, s1 = int(kv_indptr[b]), int(kv_indptr[b + 1])
+        for h in range(H):
+            if s1 <= s0:
+                continue
+            rows = np.asarray(kv_indices[s0:s1], np.int64)
+            sc = np.array([np.dot(q[b, h], np.asarray(k_deq[r], np.float64)) for r in rows]) * sm_scale
+            w = np.exp(sc - sc.max())
+            w /= w.sum()
+            out[b, h] = sum(w[i] * np.asarray(v_deq[r], np.float64) for i, r in enumerate(rows))
+    return out
+
+
+def reference_path(q_bits, kv_mode, caches, kv_indptr, kv_indices, sm_scale, threads=None):
+    """The full CPU restatement of the reference path for one decode call.
+
+    quantize Q (a2) -> dequantize Q and KV -> fp32 attention -> bf16 bits.
+    ``caches`` = dict(fp8_codes, fp8_scale, fp4_packed, fp4_scales) (numpy).
+    Returns (out_bf16_bits [B,H,512], out_f32).
+    """
+    qc, qs = quantize_fp8_per_tensor(q_bits)
+    q_deq = dequant_fp8(qc, qs)
+    k, v = dequant_kv(kv_mode, **caches)
+    out = mla_decode(q_deq, k, v, kv_indptr, kv_indices, sm_scale, threads=threads)
+    return f32_to_bf16(out), out
+
+
+def time_reference_path(q_bits, kv_mode, caches, kv_indptr, kv_indices, sm_scale,
+                        reps=3, threads=None):
+    """Median wall time (s) of ``reference_path`` after one warm-up; KV dequant included,
+    cache construction excluded.  Returns (median_s, threads_used)."""
+    import torch
+
+    threads = threads or os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    reference_path(q_bits, kv_mode, caches, kv_indptr, kv_indices, sm_scale)
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter_ns()
+        reference_path(q_bits, kv_mode, caches, kv_indptr, kv_indices, sm_scale)
+        ts.append((time.perf_counter_ns() - t0) * 1e-9)
+    ts.sort()
+    return ts[len(ts) // 2], threads
+
+
+def bf16_tensor_bits(t) -> np.ndarray:
+    """torch bf16 tensor (any device) -> numpy uint16 bits."""
+    import torch
+
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def default_sm_scale() -> float:
+    return 1.0 / math.sqrt(QK_DIM)

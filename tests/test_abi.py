@@ -1,0 +1,59 @@
+"""The C-ABI library: loads, exports every declared symbol, and rejects bad
+arguments before touching a device (no compute calls here)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from amd_optimization_challenge_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_symbols():
+    text = open(os.path.join(ROOT, "include", "mla_mi355x.h")).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+char\s*\*|int)\s+(mla_\w+)\s*\(", text, re.M)))
+
+
+def test_header_and_binding_agree():
+    syms = declared_symbols()
+    assert len(syms) >= 10
+    assert sorted(_lib.SIGNATURES) == syms
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in declared_symbols():
+        assert hasattr(lib, name), name
+    assert lib.mla_abi_version() == 1
+
+
+def test_argument_errors_without_device():
+    lib = _lib.load()
+    n = ctypes.c_int64(0)
+    assert lib.mla_workspace_bytes(4, 24, 0, ctypes.byref(n)) == _lib.MLA_ERR_UNSUPPORTED
+    assert b"num_heads" in lib.mla_last_error()
+    assert lib.mla_workspace_bytes(0, 16, 0, ctypes.byref(n)) == _lib.MLA_ERR_INVALID_ARGUMENT
+    assert lib.mla_workspace_bytes(4, 128, 1, ctypes.byref(n)) == _lib.MLA_ERR_UNSUPPORTED
+    assert lib.mla_workspace_bytes(4, 16, 7, ctypes.byref(n)) == _lib.MLA_ERR_INVALID_ARGUMENT
+    assert lib.mla_pack_mxfp4(None, 4, 33, 66, None, 16, None, 2, None) == _lib.MLA_ERR_INVALID_ARGUMENT
+    assert lib.mla_quant_fp8_per_tensor(None, 0, None, None, None, 0, None) == _lib.MLA_ERR_INVALID_ARGUMENT
+    assert lib.mla_selftest(0, None, None, None) == _lib.MLA_ERR_INVALID_ARGUMENT
+    with pytest.raises(_lib.MlaLibraryError):
+        _lib.check(lib.mla_workspace_bytes(4, 24, 0, ctypes.byref(n)), "mla_workspace_bytes")
+
+
+def test_custom_kernel_rejects_unsupported_configs_before_launch():
+    import torch
+
+    from amd_optimization_challenge_amd import custom_kernel
+
+    q = torch.zeros((2, 16, 576), dtype=torch.bfloat16)
+    indptr = torch.tensor([0, 1, 2], dtype=torch.int32)
+    with pytest.raises(NotImplementedError):
+        custom_kernel((q, {}, indptr, indptr, {"q_seq_len": 2}))
+    with pytest.raises(ValueError):
+        custom_kernel((q, {}, indptr, indptr, {"num_heads": 128}))
+    with pytest.raises(ValueError):  # CPU tensors: the HIP path refuses them
+        custom_kernel((q, {"fp8": (q, q)}, indptr, indptr, {}))
