@@ -67,16 +67,23 @@ int check_shape(int batch, int num_heads, int kv_mode) {
 
 }  // namespace
 
-int target_items_for(int num_heads, int kv_mode, int num_cu) {
-  // one resident work-group per item: H=16 fp8-V kernels fit two per CU
-  if (num_heads == 16 && kv_mode != MLA_KV_MXFP4) return 2 * num_cu;
-  return num_cu;
+// Items the planner aims for: one per resident work-group slot (H=16 fp8-V
+// kernels fit two per CU, the others one), raised to 2 per sequence when the
+// batch is large so long sequences still get split, capped at 4 rounds.
+int target_items_for(int batch, int num_heads, int kv_mode, int num_cu) {
+  const int slots = (num_heads == 16 && kv_mode != MLA_KV_MXFP4) ? 2 * num_cu : num_cu;
+  int t = 2 * batch > slots ? 2 * batch : slots;
+  return t < 4 * slots ? t : 4 * slots;
 }
 
 WsLayout workspace_layout(int batch, int num_heads, int kv_mode, int num_cu) {
   WsLayout L;
-  L.target_items = target_items_for(num_heads, kv_mode, num_cu);
-  L.max_items = 2 * num_cu + batch;  // >= target + batch for every mode
+  L.target_items = target_items_for(batch, num_heads, kv_mode, num_cu);
+  // bound on max(target, batch) over every kv_mode, so the layout (which
+  // mla_combine recomputes without a mode) is mode-independent
+  int mi = 2 * batch > 2 * num_cu ? 2 * batch : 2 * num_cu;
+  mi = mi < 8 * num_cu ? mi : 8 * num_cu;
+  L.max_items = mi > batch ? mi : batch;
   int64_t off = 0;
   L.quant_off = off;
   off = align256(off + kQuantScratchBytes);

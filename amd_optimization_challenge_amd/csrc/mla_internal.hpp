@@ -25,7 +25,7 @@ struct WsLayout {
   int target_items;
 };
 
-int target_items_for(int num_heads, int kv_mode, int num_cu);
+int target_items_for(int batch, int num_heads, int kv_mode, int num_cu);
 WsLayout workspace_layout(int batch, int num_heads, int kv_mode, int num_cu);
 
 // quant.hip

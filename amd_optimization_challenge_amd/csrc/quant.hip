@@ -177,62 +177,149 @@ __global__ __launch_bounds__(256) void pack_mxfp4_kernel(const uint8_t* __restri
 
 // ---------------------------------------------------------------------------
 // split planner (one block of 256 threads)
-// chunk = max(64, roundup64(ceil(T / target_items))); every sequence is cut
-// into n_b = ceil(L_b / chunk) near-equal pieces (1 piece if empty).  Pieces of
-// a sequence are consecutive items; a sequence with n_b == 1 writes its output
-// directly (slot -1), otherwise each piece owns partial slot = its item index.
-// Item count <= target_items + batch, which sizes the decode grid.
+// chunk = the smallest multiple of 64 tokens for which the item count
+// sum_b max(1, ceil(L_b / chunk)) fits target_items (or the longest sequence,
+// if even one item per sequence exceeds it).  Sequence b is cut into
+// n_b = ceil(L_b / chunk) near-equal pieces (1 piece if empty).  Pieces of a
+// sequence are consecutive items; sequences are laid out longest piece first
+// (for batch <= 1024) so late-starting work-groups get the short items.  A
+// sequence with n_b == 1 writes its output directly (slot -1); otherwise each
+// piece owns partial slot = its item index.
 // ---------------------------------------------------------------------------
+constexpr int kPlanSortMax = 1024;
+
+__device__ long long block_sum_ll(long long v, long long* red) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return red[0] + red[1] + red[2] + red[3];
+}
+
+__device__ int block_max_i(int v, int* red) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = max(v, __shfl_xor(v, off, 64));
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return max(max(red[0], red[1]), max(red[2], red[3]));
+}
+
 __device__ void build_plan(const int32_t* __restrict__ kv_indptr, int batch, int target_items,
                            int max_items, int32_t* __restrict__ plan) {
   __shared__ long long s_red[4];
+  __shared__ int s_redi[4];
+  __shared__ int s_n[kPlanSortMax];  // item counts in layout order, then their exclusive scan
   __shared__ int s_scan[256];
   __shared__ int s_carry;
   const int tid = threadIdx.x;
   long long tsum = 0;
-  for (int b = tid; b < batch; b += 256) tsum += (long long)max(kv_indptr[b + 1] - kv_indptr[b], 0);
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) tsum += __shfl_xor(tsum, off, 64);
-  if ((tid & 63) == 0) s_red[tid >> 6] = tsum;
+  int lmax = 0;
+  for (int b = tid; b < batch; b += 256) {
+    const int L = max(kv_indptr[b + 1] - kv_indptr[b], 0);
+    tsum += L;
+    lmax = max(lmax, L);
+  }
+  const long long total = block_sum_ll(tsum, s_red);
+  lmax = block_max_i(lmax, s_redi);
+  // binary search on chunk / 64 in [1, ceil(lmax / 64)]
+  int lo = 1, hi = max(1, (lmax + kTile - 1) / kTile);
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    const long long c = (long long)mid * kTile;
+    long long cnt = 0;
+    for (int b = tid; b < batch; b += 256) {
+      const long long L = max(kv_indptr[b + 1] - kv_indptr[b], 0);
+      cnt += L > 0 ? (L + c - 1) / c : 1;
+    }
+    cnt = block_sum_ll(cnt, s_red);
+    if (cnt <= target_items) hi = mid;
+    else lo = mid + 1;
+  }
+  const long long chunk = (long long)lo * kTile;
+  int4* items = reinterpret_cast<int4*>(plan + kPlanHeader);
+  int2* binfo = reinterpret_cast<int2*>(plan + kPlanHeader + 4 * max_items);
   if (tid == 0) s_carry = 0;
   __syncthreads();
-  const long long total = s_red[0] + s_red[1] + s_red[2] + s_red[3];
-  long long chunk = (total + target_items - 1) / max(target_items, 1);
-  chunk = ((chunk + kTile - 1) / kTile) * kTile;
-  if (chunk < kTile) chunk = kTile;
-  int4* items = reinterpret_cast<int4*>(plan + kPlanHeader);
-  // batch_info follows the item array
-  int2* binfo = reinterpret_cast<int2*>(plan + kPlanHeader + 4 * max_items);
-  for (int base = 0; base < batch; base += 256) {
-    const int b = base + tid;
-    int len = 0, nb = 0;
-    if (b < batch) {
-      len = max(kv_indptr[b + 1] - kv_indptr[b], 0);
-      nb = len > 0 ? (int)((len + chunk - 1) / chunk) : 1;
+  if (batch <= kPlanSortMax) {
+    // rank sequences by piece length, longest first (ties by index)
+    for (int b = tid; b < batch; b += 256) {
+      const int L = max(kv_indptr[b + 1] - kv_indptr[b], 0);
+      const int nb = L > 0 ? (int)((L + chunk - 1) / chunk) : 1;
+      const int piece = (L + nb - 1) / nb;
+      int rank = 0;
+      for (int b2 = 0; b2 < batch; ++b2) {
+        const int L2 = max(kv_indptr[b2 + 1] - kv_indptr[b2], 0);
+        const int n2 = L2 > 0 ? (int)((L2 + chunk - 1) / chunk) : 1;
+        const int p2 = (L2 + n2 - 1) / n2;
+        rank += (p2 > piece) || (p2 == piece && b2 < b);
+      }
+      s_n[rank] = nb;
+      binfo[b] = make_int2(rank, nb);  // rank for now; first item below
     }
-    // inclusive scan of nb across the block
-    s_scan[tid] = nb;
     __syncthreads();
-    for (int off = 1; off < 256; off <<= 1) {
-      int v = tid >= off ? s_scan[tid - off] : 0;
+    // exclusive scan of s_n in place, 256 at a time
+    for (int base = 0; base < batch; base += 256) {
+      const int i = base + tid;
+      const int v = i < batch ? s_n[i] : 0;
+      s_scan[tid] = v;
       __syncthreads();
-      s_scan[tid] += v;
+      for (int off = 1; off < 256; off <<= 1) {
+        const int a = tid >= off ? s_scan[tid - off] : 0;
+        __syncthreads();
+        s_scan[tid] += a;
+        __syncthreads();
+      }
+      if (i < batch) s_n[i] = s_carry + s_scan[tid] - v;
+      __syncthreads();
+      if (tid == 255) s_carry += s_scan[255];
       __syncthreads();
     }
-    const int first = s_carry + s_scan[tid] - nb;
-    if (b < batch) {
+    for (int b = tid; b < batch; b += 256) {
+      const int2 rb = binfo[b];
+      const int first = s_n[rb.x], nb = rb.y;
+      const int L = max(kv_indptr[b + 1] - kv_indptr[b], 0);
       const int s0 = kv_indptr[b];
       binfo[b] = make_int2(first, nb);
       for (int i = 0; i < nb; ++i) {
-        int t0 = s0 + (int)(((long long)i * len) / nb);
-        int t1 = s0 + (int)(((long long)(i + 1) * len) / nb);
+        const int t0 = s0 + (int)(((long long)i * L) / nb);
+        const int t1 = s0 + (int)(((long long)(i + 1) * L) / nb);
         items[first + i] = make_int4(b, t0, t1, nb > 1 ? first + i : -1);
       }
     }
-    __syncthreads();
-    if (tid == 255) s_carry += s_scan[255];
-    __syncthreads();
+  } else {
+    for (int base = 0; base < batch; base += 256) {
+      const int b = base + tid;
+      int L = 0, nb = 0;
+      if (b < batch) {
+        L = max(kv_indptr[b + 1] - kv_indptr[b], 0);
+        nb = L > 0 ? (int)((L + chunk - 1) / chunk) : 1;
+      }
+      s_scan[tid] = nb;
+      __syncthreads();
+      for (int off = 1; off < 256; off <<= 1) {
+        const int a = tid >= off ? s_scan[tid - off] : 0;
+        __syncthreads();
+        s_scan[tid] += a;
+        __syncthreads();
+      }
+      const int first = s_carry + s_scan[tid] - nb;
+      if (b < batch) {
+        const int s0 = kv_indptr[b];
+        binfo[b] = make_int2(first, nb);
+        for (int i = 0; i < nb; ++i) {
+          const int t0 = s0 + (int)(((long long)i * L) / nb);
+          const int t1 = s0 + (int)(((long long)(i + 1) * L) / nb);
+          items[first + i] = make_int4(b, t0, t1, nb > 1 ? first + i : -1);
+        }
+      }
+      __syncthreads();
+      if (tid == 255) s_carry += s_scan[255];
+      __syncthreads();
+    }
   }
+  __syncthreads();
   if (tid == 0) {
     plan[0] = s_carry;
     plan[1] = (int)chunk;

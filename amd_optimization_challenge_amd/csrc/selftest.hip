@@ -30,7 +30,18 @@ __global__ void selftest_kernel(int which, const uint8_t* __restrict__ in, uint8
       for (int i = 4; i < 8; ++i) a[i] = 0;
       sc = As[(l % 16) * 4 + (l / 16)];
     }
-    for (int i = 0; i < 8; ++i) b[i] = (int)gather4(B, 16, 32 * (l / 16) + 4 * i, l % 16);
+    if (which == 0) {
+      for (int i = 0; i < 8; ++i) b[i] = (int)gather4(B, 16, 32 * (l / 16) + 4 * i, l % 16);
+    } else {  // fp8 partner order of the fp4 operand: byte j of group g <-> K = 16g + (j&15) + 64(j>>4)
+      for (int i = 0; i < 8; ++i) {
+        uint32_t wd = 0;
+        for (int bb = 0; bb < 4; ++bb) {
+          const int j = 4 * i + bb, k = 16 * (l / 16) + (j & 15) + 64 * (j >> 4);
+          wd |= (uint32_t)B[k * 16 + (l % 16)] << (8 * bb);
+        }
+        b[i] = (int)wd;
+      }
+    }
     v4f c = v4f{0.f, 0.f, 0.f, 0.f};
     c = which == 0 ? mfma16_f8(a, b, c) : mfma16_f4f8(a, sc, b, c);
     for (int r = 0; r < 4; ++r) D[(4 * (l / 16) + r) * 16 + (l % 16)] = c[r];
@@ -50,7 +61,18 @@ __global__ void selftest_kernel(int which, const uint8_t* __restrict__ in, uint8
       for (int i = 4; i < 8; ++i) a[i] = 0;
       sc = As[(l % 32) * 2 + (l / 32)];
     }
-    for (int i = 0; i < 8; ++i) b[i] = (int)gather4(B, 32, 32 * (l / 32) + 4 * i, l % 32);
+    if (which == 1) {
+      for (int i = 0; i < 8; ++i) b[i] = (int)gather4(B, 32, 32 * (l / 32) + 4 * i, l % 32);
+    } else {  // fp8 partner order of the fp4 operand: byte j of group g <-> K = 16g + (j&15) + 32(j>>4)
+      for (int i = 0; i < 8; ++i) {
+        uint32_t wd = 0;
+        for (int bb = 0; bb < 4; ++bb) {
+          const int j = 4 * i + bb, k = 16 * (l / 32) + (j & 15) + 32 * (j >> 4);
+          wd |= (uint32_t)B[k * 32 + (l % 32)] << (8 * bb);
+        }
+        b[i] = (int)wd;
+      }
+    }
     v16f c = v16f{};
     c = which == 1 ? mfma32_f8(a, b, c) : mfma32_f4f8(a, sc, b, c);
     for (int r = 0; r < 16; ++r) D[(8 * (r / 4) + 4 * (l / 32) + (r % 4)) * 32 + (l % 32)] = c[r];
@@ -90,11 +112,62 @@ __global__ void selftest_kernel(int which, const uint8_t* __restrict__ in, uint8
   } else if (which == 9) {  // software f32 -> e4m3fn: 256 floats -> 256 bytes
     const float* x = reinterpret_cast<const float*>(in);
     for (int i = 0; i < 4; ++i) out[4 * l + i] = (uint8_t)f32_to_e4m3fn(x[4 * l + i]);
+  } else if (which == 10) {  // hardware e4m3fn -> f32: 64 words -> 256 floats
+    const int word = reinterpret_cast<const int*>(in)[l];
+    const v2f lo = __builtin_amdgcn_cvt_pk_f32_fp8(word, false);
+    const v2f hi = __builtin_amdgcn_cvt_pk_f32_fp8(word, true);
+    float* o = reinterpret_cast<float*>(out);
+    o[4 * l + 0] = lo[0];
+    o[4 * l + 1] = lo[1];
+    o[4 * l + 2] = hi[0];
+    o[4 * l + 3] = hi[1];
+  }
+}
+
+// One-hot probe of the fp4 operand: for each of the 128 (16x16x128) or 64
+// (32x32x64) fp4 element positions p of row 0 (lane group g = p / 32, element
+// e = p % 32 at byte e/2, low nibble for even e) set that element to 1.0 and
+// multiply by an fp8 B whose column n holds bit n of the logical K index
+// (B lanes built with the fp8 layout).  out[p*8 + n] = D[0][n].
+__global__ void fp4_probe_kernel(int big, float* __restrict__ out) {
+  const int l = threadIdx.x;
+  const int M = big ? 32 : 16;
+  const int npos = big ? 64 : 128;
+  for (int pidx = 0; pidx < npos; ++pidx) {
+    const int g = pidx / 32, e = pidx % 32;
+    v8i a = v8i{0, 0, 0, 0, 0, 0, 0, 0};
+    if (l % M == 0 && l / M == g) {
+      const uint32_t code = 2u;  // e2m1 1.0
+      a[(e / 2) / 4] = (int)(code << (8 * ((e / 2) % 4) + 4 * (e % 2)));
+    }
+    v8i bv;
+    for (int i = 0; i < 8; ++i) {
+      uint32_t w = 0;
+      for (int bb = 0; bb < 4; ++bb) {
+        const int k = 32 * (l / M) + 4 * i + bb;  // logical K under the fp8 layout
+        const int n = l % M;
+        const uint32_t one = 0x38u;  // e4m3 1.0
+        w |= (((k >> n) & 1) && n < 8 ? one : 0u) << (8 * bb);
+      }
+      bv[i] = (int)w;
+    }
+    if (!big) {
+      v4f c = mfma16_f4f8(a, 127, bv, v4f{0.f, 0.f, 0.f, 0.f});
+      if (l < 8) out[pidx * 8 + l] = c[0];
+    } else {
+      v16f c = mfma32_f4f8(a, 127, bv, v16f{});
+      if (l < 8) out[pidx * 8 + l] = c[0];
+    }
   }
 }
 
 hipError_t launch_selftest(int which, const void* in, void* out, hipStream_t stream) {
-  if (which < 0 || which > 9) return hipErrorInvalidValue;
+  if (which == 11 || which == 12) {
+    hipLaunchKernelGGL(fp4_probe_kernel, dim3(1), dim3(64), 0, stream, which == 12 ? 1 : 0,
+                       static_cast<float*>(out));
+    return hipGetLastError();
+  }
+  if (which < 0 || which > 10) return hipErrorInvalidValue;
   hipLaunchKernelGGL(selftest_kernel, dim3(1), dim3(64), 0, stream, which,
                      static_cast<const uint8_t*>(in), static_cast<uint8_t*>(out));
   return hipGetLastError();

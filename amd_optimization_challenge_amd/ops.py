@@ -207,3 +207,49 @@ def decode_fwd(q, kv_data, kv_indptr, kv_indices, sm_scale, kv_mode="fp8", out=N
 def selftest(which: int, inp: torch.Tensor, out: torch.Tensor) -> None:
     with torch.cuda.device(inp.device):
         _lib.check(_lib.load().mla_selftest(which, _ptr(inp), _ptr(out), _stream()), "mla_selftest")
+
+
+# ---------------------------------------------------------------------------
+# workspace introspection (mirrors workspace_layout() in csrc/abi.hip)
+# ---------------------------------------------------------------------------
+PLAN_HEADER = 16
+QUANT_SCRATCH = 8192
+
+
+def _a256(x: int) -> int:
+    return (x + 255) & ~255
+
+
+def workspace_layout(batch: int, num_heads: int, kv_mode, num_cu: int) -> dict:
+    """Byte offsets of the workspace regions; ``total`` equals mla_workspace_bytes."""
+    mode = kv_mode_id(kv_mode)
+    slots = 2 * num_cu if (num_heads == 16 and mode != 1) else num_cu
+    target = min(max(slots, 2 * batch), 4 * slots)
+    max_items = max(min(max(2 * num_cu, 2 * batch), 8 * num_cu), batch)
+    off = 0
+    lay = {"quant": off}
+    off = _a256(off + QUANT_SCRATCH)
+    lay["q_fp8"] = off
+    off = _a256(off + batch * num_heads * QK_DIM)
+    lay["plan"] = off
+    off = _a256(off + (PLAN_HEADER + 4 * max_items + 2 * batch) * 4)
+    lay["part_o"] = off
+    off = _a256(off + max_items * num_heads * V_DIM * 4)
+    lay["part_lse"] = off
+    off = _a256(off + max_items * num_heads * 4)
+    lay.update(total=off, max_items=max_items, target_items=target)
+    return lay
+
+
+def read_plan(ws: torch.Tensor, batch: int, num_heads: int, kv_mode) -> dict:
+    """Copy the device plan back to the host (synchronizes; for tests and tooling)."""
+    lay = workspace_layout(batch, num_heads, kv_mode, cu_count())
+    mi = lay["max_items"]
+    n_words = PLAN_HEADER + 4 * mi + 2 * batch
+    words = ws[lay["plan"]: lay["plan"] + 4 * n_words].view(torch.int32).cpu()
+    hdr = words[:PLAN_HEADER]
+    n = int(hdr[0])
+    items = words[PLAN_HEADER: PLAN_HEADER + 4 * mi].reshape(mi, 4)[:n]
+    binfo = words[PLAN_HEADER + 4 * mi:].reshape(batch, 2)
+    return {"num_items": n, "chunk": int(hdr[1]), "total": int(hdr[2]), "batch": int(hdr[3]),
+            "max_items": int(hdr[4]), "items": items, "batch_info": binfo, "layout": lay}

@@ -1,0 +1,157 @@
+"""Pins, on the device, the MFMA operand/accumulator layouts and conversion
+semantics the decode kernels rely on (csrc/selftest.hip), against numpy."""
+import numpy as np
+import pytest
+import torch
+
+from amd_optimization_challenge_amd import ops
+from oracle import mla_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+IN_BYTES = {0: 4096, 1: 4096, 2: 3136, 3: 3136, 4: 1024, 5: 2048, 6: 1024, 7: 512, 8: 1024, 9: 1024,
+            10: 256, 11: 0, 12: 0}
+
+
+def run(which, inp: np.ndarray, out_bytes: int) -> np.ndarray:
+    print(f"selftest {which}", flush=True)
+    assert np.ascontiguousarray(inp).nbytes == IN_BYTES[which] or (IN_BYTES[which] == 0), "input size"
+    i = torch.from_numpy(np.ascontiguousarray(inp).view(np.uint8).reshape(-1)).cuda()
+    o = torch.zeros(out_bytes, dtype=torch.uint8, device="cuda")
+    ops.selftest(which, i, o)
+    torch.cuda.synchronize()
+    return o.cpu().numpy()
+
+
+def fp8_codes(rng, shape):
+    # exponent field 5..9 (values 2^-2 .. 2^2 * (1 + m/8)), random sign
+    e = rng.integers(5, 10, shape)
+    m = rng.integers(0, 8, shape)
+    s = rng.integers(0, 2, shape)
+    return ((s << 7) | (e << 3) | m).astype(np.uint8)
+
+
+@pytest.mark.parametrize("which,M,N,K", [(0, 16, 16, 128), (1, 32, 32, 64), (4, 16, 16, 32)])
+def test_mfma_fp8_layouts(cuda, which, M, N, K):
+    rng = np.random.default_rng(which)
+    A = fp8_codes(rng, (M, K))
+    B = fp8_codes(rng, (K, N))
+    D = run(which, np.concatenate([A.reshape(-1), B.reshape(-1)]), M * N * 4).view(np.float32).reshape(M, N)
+    Af, Bf = O.e4m3fn_to_f32(A).astype(np.float64), O.e4m3fn_to_f32(B).astype(np.float64)
+    ref = Af @ Bf
+    # the MFMA does not round like a sequential f32 sum; bound the error by the
+    # magnitude of the products (a wrong layout misses by O(1) of that scale)
+    scale = np.abs(Af) @ np.abs(Bf)
+    assert np.all(np.abs(D - ref) <= 1e-4 * scale), np.max(np.abs(D - ref) / scale)
+
+
+@pytest.mark.parametrize("which,M,N,K", [(2, 16, 16, 128), (3, 32, 32, 64)])
+def test_mfma_scaled_fp4_by_fp8_layouts(cuda, which, M, N, K):
+    rng = np.random.default_rng(10 + which)
+    Ap = rng.integers(0, 256, (M, K // 2), dtype=np.uint8)
+    As = rng.integers(123, 131, (M, K // 32), dtype=np.uint8)
+    B = fp8_codes(rng, (K, N))
+    inp = np.concatenate([Ap.reshape(-1), As.reshape(-1), B.reshape(-1)])
+    D = run(which, inp, M * N * 4).view(np.float32).reshape(M, N)
+    Bf = O.e4m3fn_to_f32(B).astype(np.float64)
+    # the kernel builds B in the fp8 partner order of the fp4 operand (see
+    # expected_kmap), so D must equal the natural product; other candidates
+    # are reported for diagnosis
+    swapped = ((Ap >> 4) | (Ap << 4)).astype(np.uint8)
+    hyps = {
+        "low-nibble-first, scaled": O.dequant_mxfp4(Ap, As, K),
+        "high-nibble-first, scaled": O.dequant_mxfp4(swapped, As, K),
+        "low-nibble-first, unscaled": O.dequant_mxfp4(Ap, np.full_like(As, 127), K),
+        "high-nibble-first, unscaled": O.dequant_mxfp4(swapped, np.full_like(As, 127), K),
+    }
+    errs = {}
+    for name, Af in hyps.items():
+        ref = Af.astype(np.float64) @ Bf
+        scale = np.abs(Af.astype(np.float64)) @ np.abs(Bf) + 1e-30
+        errs[name] = float(np.max(np.abs(D - ref) / scale))
+    print("fp4 hypotheses (max err / scale):", errs, flush=True)
+    assert errs["low-nibble-first, scaled"] <= 1e-4, errs
+
+
+def test_mfma_bf16_layout(cuda):
+    rng = np.random.default_rng(5)
+    A = O.f32_to_bf16(rng.integers(-8, 9, (16, 32)).astype(np.float32) / 4)
+    B = O.f32_to_bf16(rng.integers(-8, 9, (32, 16)).astype(np.float32) / 4)
+    D = run(5, np.concatenate([A.reshape(-1), B.reshape(-1)]), 16 * 16 * 4).view(np.float32).reshape(16, 16)
+    ref = O.bf16_to_f32(A).astype(np.float64) @ O.bf16_to_f32(B).astype(np.float64)
+    np.testing.assert_allclose(D, ref, rtol=0, atol=1e-6)
+
+
+def test_hw_fp8_pack_is_ocp_rne(cuda):
+    rng = np.random.default_rng(6)
+    grid = O.E4M3FN[:127]
+    mids = ((grid[:-1] + grid[1:]) / 2).astype(np.float32)
+    x = np.concatenate([mids[:120], rng.uniform(0, 256, 136).astype(np.float32)])[:256]
+    got = run(6, x.astype(np.float32), 256)
+    assert np.array_equal(got, O.f32_to_e4m3fn(x))
+
+
+def test_hw_fp4_to_bf16_scaled(cuda):
+    rng = np.random.default_rng(7)
+    words = rng.integers(0, 2 ** 32, 64, dtype=np.uint64).astype(np.uint32)
+    scales = np.exp2(rng.integers(-6, 7, 64)).astype(np.float32)
+    got = run(7, np.concatenate([words.view(np.uint8), scales.view(np.uint8)]), 64 * 4 * 4).view(np.uint32)
+    mag = np.array([0, .5, 1, 1.5, 2, 3, 4, 6], np.float64)
+    exp = np.zeros(256, np.uint32)
+    for l in range(64):
+        for j in range(4):
+            byte = (int(words[l]) >> (8 * j)) & 0xFF
+            vals = []
+            for nib in (byte & 0xF, byte >> 4):
+                v = (-1 if nib & 8 else 1) * mag[nib & 7] * scales[l]
+                vals.append(int(O.f32_to_bf16(np.array([v], np.float32))[0]))
+            exp[4 * l + j] = vals[0] | (vals[1] << 16)
+    assert np.array_equal(got, exp)
+
+
+def test_byte_transpose(cuda):
+    rng = np.random.default_rng(8)
+    x = rng.integers(0, 2 ** 32, (64, 4), dtype=np.uint64).astype(np.uint32)
+    got = run(8, x, 64 * 16).view(np.uint32).reshape(64, 4)
+    xb = x.view(np.uint8).reshape(64, 4, 4)  # [lane][row r][byte e]
+    exp = np.ascontiguousarray(xb.transpose(0, 2, 1)).view(np.uint32).reshape(64, 4)
+    assert np.array_equal(got, exp)
+
+
+def test_hw_fp8_decode(cuda):
+    words = np.arange(256, dtype=np.uint8).reshape(64, 4).copy()
+    got = run(10, words, 256 * 4).view(np.float32)
+    ref = O.e4m3fn_to_f32(np.arange(256))
+    ok = (got == ref) | (np.isnan(got) & np.isnan(ref))
+    assert ok.all(), np.nonzero(~ok)
+
+
+def test_software_e4m3fn_encoder(cuda):
+    rng = np.random.default_rng(9)
+    grid = O.E4M3FN[:127]
+    mids = ((grid[:-1] + grid[1:]) / 2).astype(np.float32)
+    x = np.concatenate([mids, -mids[:3], rng.uniform(-448, 448, 256).astype(np.float32)])[:256]
+    got = run(9, x.astype(np.float32), 256)
+    assert np.array_equal(got, O.f32_to_e4m3fn(x))
+
+
+# f8f6f4 MFMA with an fp4 A operand: fp4 element e of lane group g (K = 32g + e,
+# one MX block per lane) meets the fp8 B byte j of lane group g' with
+# 32g + e = 16g' + (j & 15) + S*(j >> 4), S = 64 (16x16x128) or 32 (32x32x64),
+# when fp8 bytes are numbered 32g' + j.  Pinned here by a one-hot probe.
+def expected_kmap(npos):
+    S = 64 if npos == 128 else 32
+    out = np.empty(npos, int)
+    for gp in range(npos // 32):
+        for j in range(32):
+            out[16 * gp + (j & 15) + S * (j >> 4)] = 32 * gp + j
+    return out
+
+
+@pytest.mark.parametrize("which,npos", [(11, 128), (12, 64)])
+def test_fp4_operand_k_map(cuda, which, npos):
+    """Which fp8 byte (numbered 32g' + j) each fp4 A element (32g + e) pairs with."""
+    got = run(which, np.zeros(16, np.uint8), npos * 8 * 4).view(np.float32).reshape(npos, 8)
+    kmap = (got[:, :7] > 0.5).astype(int) @ (1 << np.arange(7))
+    assert np.array_equal(kmap, expected_kmap(npos)), kmap.tolist()
