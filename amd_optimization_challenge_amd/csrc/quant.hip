@@ -211,16 +211,21 @@ __device__ void build_plan(const int32_t* __restrict__ kv_indptr, int batch, int
   __shared__ long long s_red[4];
   __shared__ int s_redi[4];
   __shared__ int s_n[kPlanSortMax];  // item counts in layout order, then their exclusive scan
+  __shared__ int s_piece[kPlanSortMax];
   __shared__ int s_scan[256];
   __shared__ int s_carry;
+  __shared__ int s_len[kPlanSortMax];
   const int tid = threadIdx.x;
+  const bool staged = batch <= kPlanSortMax;  // lengths kept in LDS
   long long tsum = 0;
   int lmax = 0;
   for (int b = tid; b < batch; b += 256) {
     const int L = max(kv_indptr[b + 1] - kv_indptr[b], 0);
+    if (staged) s_len[b] = L;
     tsum += L;
     lmax = max(lmax, L);
   }
+  auto len_of = [&](int b) { return staged ? s_len[b] : max(kv_indptr[b + 1] - kv_indptr[b], 0); };
   const long long total = block_sum_ll(tsum, s_red);
   lmax = block_max_i(lmax, s_redi);
   // binary search on chunk / 64 in [1, ceil(lmax / 64)]
@@ -230,7 +235,7 @@ __device__ void build_plan(const int32_t* __restrict__ kv_indptr, int batch, int
     const long long c = (long long)mid * kTile;
     long long cnt = 0;
     for (int b = tid; b < batch; b += 256) {
-      const long long L = max(kv_indptr[b + 1] - kv_indptr[b], 0);
+      const long long L = len_of(b);
       cnt += L > 0 ? (L + c - 1) / c : 1;
     }
     cnt = block_sum_ll(cnt, s_red);
@@ -243,51 +248,26 @@ __device__ void build_plan(const int32_t* __restrict__ kv_indptr, int batch, int
   if (tid == 0) s_carry = 0;
   __syncthreads();
   if (batch <= kPlanSortMax) {
-    // rank sequences by piece length, longest first (ties by index)
+    // piece length per sequence in LDS, then rank longest first (ties by index)
     for (int b = tid; b < batch; b += 256) {
-      const int L = max(kv_indptr[b + 1] - kv_indptr[b], 0);
+      const int L = len_of(b);
       const int nb = L > 0 ? (int)((L + chunk - 1) / chunk) : 1;
-      const int piece = (L + nb - 1) / nb;
+      s_piece[b] = (L + nb - 1) / nb;
+    }
+    __syncthreads();
+    for (int b = tid; b < batch; b += 256) {
+      const int L = len_of(b);
+      const int nb = L > 0 ? (int)((L + chunk - 1) / chunk) : 1;
+      const int piece = s_piece[b];
       int rank = 0;
       for (int b2 = 0; b2 < batch; ++b2) {
-        const int L2 = max(kv_indptr[b2 + 1] - kv_indptr[b2], 0);
-        const int n2 = L2 > 0 ? (int)((L2 + chunk - 1) / chunk) : 1;
-        const int p2 = (L2 + n2 - 1) / n2;
+        const int p2 = s_piece[b2];
         rank += (p2 > piece) || (p2 == piece && b2 < b);
       }
       s_n[rank] = nb;
       binfo[b] = make_int2(rank, nb);  // rank for now; first item below
     }
     __syncthreads();
-    // exclusive scan of s_n in place, 256 at a time
-    for (int base = 0; base < batch; base += 256) {
-      const int i = base + tid;
-      const int v = i < batch ? s_n[i] : 0;
-      s_scan[tid] = v;
-      __syncthreads();
-      for (int off = 1; off < 256; off <<= 1) {
-        const int a = tid >= off ? s_scan[tid - off] : 0;
-        __syncthreads();
-        s_scan[tid] += a;
-        __syncthreads();
-      }
-      if (i < batch) s_n[i] = s_carry + s_scan[tid] - v;
-      __syncthreads();
-      if (tid == 255) s_carry += s_scan[255];
-      __syncthreads();
-    }
-    for (int b = tid; b < batch; b += 256) {
-      const int2 rb = binfo[b];
-      const int first = s_n[rb.x], nb = rb.y;
-      const int L = max(kv_indptr[b + 1] - kv_indptr[b], 0);
-      const int s0 = kv_indptr[b];
-      binfo[b] = make_int2(first, nb);
-      for (int i = 0; i < nb; ++i) {
-        const int t0 = s0 + (int)(((long long)i * L) / nb);
-        const int t1 = s0 + (int)(((long long)(i + 1) * L) / nb);
-        items[first + i] = make_int4(b, t0, t1, nb > 1 ? first + i : -1);
-      }
-    }
   } else {
     for (int base = 0; base < batch; base += 256) {
       const int b = base + tid;
