@@ -30,6 +30,7 @@ namespace mla {
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kPScale = 256.0f;  // fp8 P = p * 256
+constexpr float kRebase = 96.0f;   // H128: max log2 distance of a tile max above the fixed reference
 
 __device__ __forceinline__ int kv_slot(const int32_t* __restrict__ idx, int pos) {
   return idx != nullptr ? idx[pos] : pos;
@@ -471,218 +472,335 @@ __global__ __launch_bounds__(256, 1) void decode_h16_kernel(const DecodeParams p
 }
 
 // ============================================================================
-// H = 128: 8 waves.  Wave w owns head group g4 = w & 3 (heads 32*g4 .. +31) and
-// half = w >> 2: it scores token half `half` of each 64-token tile (32x32x64
-// MFMAs over the 576 dims) and accumulates O^T for latent dims 256*half .. +255
-// over all 64 tokens.  The two waves of a head group swap their tile maxima and
-// their halves of P through LDS, so both run the same online softmax.
+// H = 128.  4 waves; wave w owns heads 32w .. 32w+31 for every token of the
+// work item and all 512 latent dims, so the softmax state and O^T never leave
+// the wave.  Q^T (the QK B operand) stays in registers, O^T in accumulators.
+// Cache rows are gathered straight into an LDS ring by LDS-DMA (no staging
+// registers), S tiles deep; the PV A operand (V^T) is read from the row-major
+// tile with ds_read_b64_tr_b8, so no transposed copy is ever written.
 //   KF: 0 = fp8 K rows, V = same rows; 1 = fp4 K rows + e8m0, V = fp8 cache
+// Online softmax is rescaled lazily: the exponent base m only moves when a
+// head's tile max exceeds it by more than 8 (log2 units), so P <= 2^8 fits
+// e4m3 and O^T is touched by VALU only on those (rare) tiles.
 // ============================================================================
 template <int KF>
 struct H128 {
-  static constexpr int KROW = KF == 0 ? 576 : 288;
-  static constexpr int KST = KROW + 16;
-  static constexpr int OFF_K = 0;
-  static constexpr int OFF_S = OFF_K + kTile * KST;
-  static constexpr int OFF_VT = OFF_S + (KF == 1 ? kTile * 20 : 0);
-  static constexpr int OFF_Q = OFF_VT + kVDim * 64;        // V^T rows of 64 bytes
-  static constexpr int OFF_P = OFF_Q + 128 * kQKDim;       // [hi/lo][4 groups][64 lanes][32 B]
-  static constexpr int OFF_MAX = OFF_P + 2 * 4 * 64 * 32;  // [2 halves][128] f32
-  static constexpr int OFF_L = OFF_MAX + 2 * 128 * 4;      // [2 halves][128] f32
-  static constexpr int LDS = OFF_L + 2 * 128 * 4;
-  static constexpr int NT = 512;
+  static constexpr int NT = 256;
+  static constexpr int KST = KF == 0 ? 592 : 304;              // K row stride in LDS
+  static constexpr int KCH = KF == 0 ? 36 : 18;                // real 16-B chunks per K row
+  static constexpr int VST = 528;                              // fp8 V row stride (KF == 1)
+  static constexpr int KDMA = (kTile * KST + 1023) / 1024;     // 1-KiB DMA windows: 37 / 19
+  static constexpr int VDMA = KF == 1 ? (kTile * VST + 1023) / 1024 : 0;  // 33
+  static constexpr int DPW = (KDMA + VDMA + 3) / 4;            // windows per wave: 10 / 13
+  static constexpr int STAGE = 4 * DPW * 1024;                 // ring stage bytes
+  static constexpr int S = KF == 0 ? 3 : 2;                    // ring depth (tiles)
+  static constexpr int OFF_V = KDMA * 1024;                    // V rows inside a stage (KF == 1)
+  static constexpr int OFF_SLOT = S * STAGE;                   // [S][64] int32 cache slots
+  static constexpr int OFF_VOTE = OFF_SLOT + S * 256;          // [2][4] restart votes
+  static constexpr int LDS = OFF_VOTE + 16;
 };
 
-// V^T row of latent dim d: token n sits at byte pos(n) = 32hh + 16u + 4q + i
-// (n = 32u + 8q + 4hh + i), the order of the P operand built from the 32x32
-// score accumulators.  The row's four 16-byte chunks are XOR-swizzled by
-// ((d >> 2) ^ (d >> 4)) & 3 so that both the transposed writes (dims 16 apart)
-// and the operand reads (consecutive dims) spread over the banks.
-__device__ __forceinline__ int vt128_sw(int d) { return ((d >> 2) ^ (d >> 4)) & 3; }
-__device__ __forceinline__ int vt128_quad_off(int d, int tq) {
-  const int pos = 32 * (tq & 1) + 16 * (tq >> 3) + 4 * ((tq & 7) >> 1);
-  return d * 64 + 16 * ((pos >> 4) ^ vt128_sw(d)) + (pos & 15);
-}
-// Q chunk swizzle: 16-byte chunk c (0..35) of head row h lives at chunk
-// c ^ ((h >> 2) & 3), which stays inside the row (36 is a multiple of 4).  Rows
-// are 36 chunks apart, so heads h and h+4 would otherwise hit the same banks.
-__device__ __forceinline__ int q_off(int h, int c) { return h * kQKDim + 16 * (c ^ ((h >> 2) & 3)); }
-
 template <int KF, bool IDX>
-__global__ __launch_bounds__(512, 1) void decode_h128_kernel(const DecodeParams p) {
+__global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams p) {
   using C = H128<KF>;
-  __shared__ __attribute__((aligned(16))) uint8_t smem[C::LDS];
-  uint8_t* Klds = smem + C::OFF_K;
-  uint8_t* Slds = smem + C::OFF_S;
-  uint8_t* Vt = smem + C::OFF_VT;
-  uint8_t* Qlds = smem + C::OFF_Q;
-  uint8_t* Pex = smem + C::OFF_P;
-  float* smax = reinterpret_cast<float*>(smem + C::OFF_MAX);
-  float* lsum = reinterpret_cast<float*>(smem + C::OFF_L);
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[C::LDS];
+  const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
 
   const int32_t* plan = p.plan;
   if ((int)blockIdx.x >= plan[0]) return;
   const int4 it = reinterpret_cast<const int4*>(plan + kPlanHeader)[blockIdx.x];
   const int b = it.x, t_beg = it.y, t_end = it.z, slot = it.w;
+  const int ntok = t_end - t_beg;
+  const int ntiles = (ntok + kTile - 1) / kTile;
 
   const int tid = threadIdx.x;
-  const int w = tid >> 6, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
-  const int g4 = w & 3, half = w >> 2;
-  const int head = 32 * g4 + l32;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (feeds M0)
+  const int lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
+  const int head = 32 * w + l32;
 
-  // Q [128][576] fp8 -> LDS; visible after barrier (A)
+  // ---- Q^T B operand, K-step ks = dims 64ks .. +63 (fp4 K: partner order) -----
+  v8i qv[9];
   {
-    const uint8_t* qb = p.q_fp8 + (int64_t)b * 128 * kQKDim;
-    for (int k = tid; k < 128 * 36; k += C::NT) {
-      const int h = k / 36, ch = k - h * 36;
-      *reinterpret_cast<uint4*>(Qlds + q_off(h, ch)) = *reinterpret_cast<const uint4*>(qb + h * kQKDim + 16 * ch);
+    const uint8_t* qrow = p.q_fp8 + ((int64_t)b * 128 + head) * kQKDim;
+#pragma unroll
+    for (int ks = 0; ks < 9; ++ks) {
+      const int d0 = KF == 0 ? 64 * ks + 32 * hh : 64 * ks + 16 * hh;
+      const int d1 = KF == 0 ? d0 + 16 : d0 + 32;
+      const uint4 lo = *reinterpret_cast<const uint4*>(qrow + d0);
+      const uint4 hi = *reinterpret_cast<const uint4*>(qrow + d1);
+      qv[ks] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
     }
+#pragma unroll
+    for (int ks = 0; ks < 9; ++ks) asm volatile("" : "+v"(qv[ks]));
   }
   const float qs = p.q_scale[0];
   const float kvs = p.kv_scale[0];
   const float c = qs * (KF == 0 ? kvs : 1.0f) * p.sm_scale * kLog2e;
-  const float vscale = kvs / kPScale;
+  const float vscale = kvs;  // the 2^8 carried by P' is folded into the PV scale exponent
 
-  v16f o[8];
+  v16f o[16];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) o[i] = v16f{};
-  float m_run = neg_inf(), l_run = 0.f;
+  for (int i = 0; i < 16; ++i) o[i] = v16f{};
+  float m_ref = 0.f, l_run = 0.f;
 
-  TileLoader<C::NT, KF, KF == 1 ? 1 : 0, IDX> L;
-  L.init(tid);
-  auto vt_off = [](int d, int tq) { return vt128_quad_off(d, tq); };
+  // ---- DMA issue helpers -------------------------------------------------------
+  auto slot_of = [&](int st, int tok, int pos0) -> int {
+    if constexpr (IDX) return reinterpret_cast<const int*>(smem + C::OFF_SLOT + st * 256)[tok];
+    else return min(pos0 + tok, t_end - 1);
+  };
+  auto issue_slots = [&](int t) {  // wave 0: 64 slots of tile t (positions clamped into the item)
+    if constexpr (IDX) {
+      if (w == 0) {
+        const int pos = min(t_beg + kTile * t + lane, t_end - 1);
+        dma4_to_lds(p.kv_indices + pos, lds0 + C::OFF_SLOT + (t % C::S) * 256);
+      }
+    }
+  };
+  auto issue_rows = [&](int t) {  // this wave's DPW windows of tile t
+    const int st = t % C::S;
+    const int pos0 = t_beg + kTile * t;
+    const uint32_t sbase = lds0 + st * C::STAGE;
+#pragma unroll
+    for (int k = 0; k < C::DPW; ++k) {
+      const int u = w + 4 * k;  // window index within the stage
+      const uint8_t* src;
+      if (u < C::KDMA) {
+        const int bb = 1024 * u + 16 * lane;
+        int tok = bb / C::KST, pos = (bb - tok * C::KST) >> 4;
+        if (tok >= kTile) { tok = kTile - 1; pos = 0; }
+        src = p.k_cache + (int64_t)slot_of(st, tok, pos0) * p.k_row_stride + 16 * min(pos, C::KCH - 1);
+      } else if (KF == 1 && u < C::KDMA + C::VDMA) {
+        const int bb = 1024 * (u - C::KDMA) + 16 * lane;
+        int tok = bb / C::VST, pos = (bb - tok * C::VST) >> 4;
+        if (tok >= kTile) { tok = kTile - 1; pos = 0; }
+        src = p.v_cache + (int64_t)slot_of(st, tok, pos0) * p.v_row_stride + 16 * min(pos, 31);
+      } else {  // padding window: any valid source
+        src = p.k_cache + (int64_t)slot_of(st, kTile - 1, pos0) * p.k_row_stride;
+      }
+      dma16_to_lds(src, sbase + 1024 * u);
+    }
+  };
+  // fp4 K scales: lane (token u*32 + l32) needs blocks 2ks + hh, ks = 0..8
+  uint32_t sc_nxt[2][9], sc_cur[2][9];
+  auto load_scales = [&](int t) {
+    if constexpr (KF == 1) {
+      const int st = t % C::S;
+      const int pos0 = t_beg + kTile * t;
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const uint8_t* srow = p.k_scales + (int64_t)slot_of(st, 32 * u + l32, pos0) * p.k_scale_stride;
+#pragma unroll
+        for (int ks = 0; ks < 9; ++ks) sc_nxt[u][ks] = srow[2 * ks + hh];
+      }
+    }
+  };
 
-  const int ntok = t_end - t_beg;
-  const int ntiles = (ntok + kTile - 1) / kTile;
-  const int last = t_end - 1;
-  if (ntiles > 0) {
-    int sl[4];
-    L.load_idx(p, t_beg, last, sl);
-    L.load_rows(p, sl, min(kTile, ntok));
-    L.load_idx(p, t_beg + kTile, last, L.sl_nxt);
+  auto prologue = [&]() {
+    // prologue: slots(0) visible; rows(0) [+ scales(0)] in flight; slots(1), and for S = 3
+    // rows(1) and slots(2), issued in the order the steady-state waits assume
+    issue_slots(0);
+    wait_vmcnt<0>();
+    lds_barrier();
+    issue_slots(1);
+    issue_rows(0);
+    load_scales(0);
+    if constexpr (C::S == 3) {
+      if (ntiles > 1) {
+        wait_vmcnt<C::DPW>();  // slots(1) landed (rows(0) may still be in flight)
+        lds_barrier();
+        issue_slots(2);
+        issue_rows(1);
+      }
+    }
+  };
+
+  // lane-constant parts of the transpose-read addresses (PV A operand)
+  const int vrow_st = KF == 0 ? C::KST : C::VST;
+  const int voff = KF == 0 ? 0 : C::OFF_V;
+  int tr_off[4];
+  {
+    const int G = lane >> 4, m = (lane & 15) >> 1, oo = lane & 1;
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) {
+      const int k = 8 * cc + m;  // K-slot of this lane half
+      const int T = 32 * (k >> 4) + 8 * ((k >> 2) & 3) + 4 * hh + (k & 3);
+      tr_off[cc] = voff + T * vrow_st + 16 * (G & 1) + 8 * oo;
+    }
   }
 
-  auto tile = [&](auto pf, int ti) {
-    constexpr bool PF = decltype(pf)::value;
-    const int t0 = ti * kTile;
-    const int nval = min(kTile, ntok - t0);
-    L.store_k(Klds, C::KST, Slds);
-    L.store_v_fp8(Vt, vt_off);
-    __syncthreads();  // (A) tile (and Q) visible
-    if constexpr (PF) {
-      L.load_rows(p, L.sl_nxt, min(kTile, ntok - t0 - kTile));
-      L.load_idx(p, t_beg + t0 + 2 * kTile, last, L.sl_nxt);
+  // O^T accumulates sum_n V_n 2^(s_n - m_ref) against a fixed per-lane (head)
+  // reference, the first tile's ceil(max); a tile's own offset rides on the
+  // B-operand e8m0 scale of the PV MFMA, so the accumulators are never
+  // rescaled.  A tile whose max lies more than kRebase above m_ref (the
+  // accumulators could overflow) makes the whole block restart the item with
+  // m_ref = the running max: a block-wide vote through LDS, one tile late.
+  volatile uint8_t* vote = smem + C::OFF_VOTE;  // [2][4] wave flags, double-buffered by tile parity
+  float m_seen = neg_inf();
+  bool have_ref = false;
+  for (;;) {
+  if (ntiles > 0) prologue();
+  bool restart = false;
+  for (int ti = 0; ti < ntiles; ++ti) {
+    const int st = ti % C::S;
+    const int nval = min(kTile, ntok - kTile * ti);
+    // tile ti landed (and slots for the tile issued next); see the prologue order
+    if constexpr (C::S == 3) {
+      if (ti + 1 < ntiles) wait_vmcnt<C::DPW>();
+      else wait_vmcnt<0>();
+    } else {
+      wait_vmcnt<0>();
+    }
+    if constexpr (KF == 1) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int ks = 0; ks < 9; ++ks) sc_cur[u][ks] = sc_nxt[u][ks];
+    }
+    lds_barrier();  // tile ti visible; the stage of tile ti-1 is free
+    if (ti > 0 && __builtin_amdgcn_readfirstlane(*reinterpret_cast<volatile uint32_t*>(vote + 4 * ((ti - 1) & 1))) != 0) {
+      restart = true;
+      break;
+    }
+    if (ti + C::S - 1 < ntiles) {
+      issue_slots(ti + C::S);
+      issue_rows(ti + C::S - 1);
+      if constexpr (KF == 1) load_scales(ti + C::S - 1);
     }
 
-    // ---- scores S^T for tokens 32*half .. +31 of this tile, heads of g4 -------
-    v16f s = v16f{};
-    const int trow = 32 * half + l32;
+    // ---- scores S^T: s0 = tokens 0..31, s1 = tokens 32..63 of the tile ------------
+    const uint32_t sb = lds0 + st * C::STAGE;
+    const uint8_t* kt = smem + st * C::STAGE;
+    v16f s0 = v16f{}, s1 = v16f{};
+    // one K-step of lookahead on the LDS fragments; sched_barrier keeps the
+    // compiler from hoisting every fragment load (register blow-up)
+    auto kfrag = [&](int ks, int u) -> v8i {
+      if constexpr (KF == 0) return ld_v8(kt + (32 * u + l32) * C::KST + 64 * ks + 32 * hh);
+      else return ld_v4_as_v8(kt + (32 * u + l32) * C::KST + 16 * (2 * ks + hh));
+    };
+    v8i a0n = kfrag(0, 0), a1n = kfrag(0, 1);
 #pragma unroll
     for (int ks = 0; ks < 9; ++ks) {
-      // Q chunks of this lane's head for K-step ks: fp8 K pairs dims 64ks+32hh..+31;
-      // fp4 K pairs dims 64ks+16hh..+15 and 64ks+32+16hh..+15 (f8f6f4 fp4 order)
-      const int qc0 = KF == 0 ? 4 * ks + 2 * hh : 4 * ks + hh;
-      const int qc1 = KF == 0 ? qc0 + 1 : qc0 + 2;
-      v8i qf;
-      {
-        const uint4 a = *reinterpret_cast<const uint4*>(Qlds + q_off(head, qc0));
-        const uint4 bq = *reinterpret_cast<const uint4*>(Qlds + q_off(head, qc1));
-        qf[0] = a.x; qf[1] = a.y; qf[2] = a.z; qf[3] = a.w;
-        qf[4] = bq.x; qf[5] = bq.y; qf[6] = bq.z; qf[7] = bq.w;
+      const v8i a0 = a0n, a1 = a1n;
+      if (ks < 8) {
+        a0n = kfrag(ks + 1, 0);
+        a1n = kfrag(ks + 1, 1);
       }
       if constexpr (KF == 0) {
-        s = mfma32_f8(ld_v8(Klds + trow * C::KST + 64 * ks + 32 * hh), qf, s);
+        s0 = mfma32_f8(a0, qv[ks], s0);
+        s1 = mfma32_f8(a1, qv[ks], s1);
       } else {
-        const int blk = 2 * ks + hh;
-        s = mfma32_f4f8(ld_v4_as_v8(Klds + trow * C::KST + 16 * blk), (int)Slds[trow * 20 + blk], qf, s);
+        s0 = mfma32_f4f8(a0, (int)sc_cur[0][ks], qv[ks], s0);
+        s1 = mfma32_f4f8(a1, (int)sc_cur[1][ks], qv[ks], s1);
       }
+      __builtin_amdgcn_sched_barrier(0);
     }
-    // s[r] = score(token 32*half + 8(r/4) + 4hh + r%4, head)
+    (void)sb;
+    // s_u[r] = score(token 32u + 8(r/4) + 4hh + r%4, head)
     float mx = neg_inf();
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int tk = 32 * half + 8 * (r >> 2) + 4 * hh + (r & 3);
-      s[r] = tk < nval ? s[r] * c : neg_inf();
-      mx = fmaxf(mx, s[r]);
+      const int tk = 8 * (r >> 2) + 4 * hh + (r & 3);
+      s0[r] = tk < nval ? s0[r] * c : neg_inf();
+      s1[r] = 32 + tk < nval ? s1[r] * c : neg_inf();
+      mx = fmaxf(mx, fmaxf(s0[r], s1[r]));
     }
     mx = fmaxf(mx, shfl_xor_f(mx, 32));
-    if (hh == 0) smax[half * 128 + head] = mx;
-    __syncthreads();  // (B) half maxima visible
-    const float tmax = fmaxf(smax[head], smax[128 + head]);
-    const float m_new = fmaxf(m_run, tmax);
-    const float alpha = exp2f(m_run - m_new);
-    m_run = m_new;
+    // Fixed per-item reference m_ref (the first tile's ceil(max)); each tile's
+    // offset rides on the B-operand e8m0 scale of the PV MFMA, so O^T is never
+    // rescaled: O^T accumulates sum_n V_n 2^(s_n - m_ref).
+    const float m_t = __builtin_ceilf(mx);
+    if (!have_ref) m_ref = m_t;  // first tile of the first pass
+    have_ref = true;
+    m_seen = fmaxf(m_seen, m_t);
+    const bool over = __any(m_t > m_ref + kRebase);
+    if (lane == 0) vote[4 * (ti & 1) + w] = over ? 1 : 0;
+    // P' = 2^(s - m_t) * 2^8 in fp8; the e8m0 B scale 2^(m_t - m_ref - 8) restores 2^(s - m_ref)
+    const float dm = fminf(fmaxf(m_t - m_ref, -160.f), 160.f);
+    const int pscale = min(max((int)dm - 8 + 127, 0), 254);
     float psum = 0.f;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      s[r] = exp2f(s[r] - m_new);
-      psum += s[r];
+      s0[r] = exp2f(s0[r] - m_t);
+      s1[r] = exp2f(s1[r] - m_t);
+      psum += s0[r] + s1[r];
     }
-    l_run = l_run * alpha + psum;
-    // this wave's half of the P^T B operand: bytes 16*half .. +15 of the lane's 32
-    {
-      uint4 ph, pl;
-      pack4_fp8_split(s[0] * kPScale, s[1] * kPScale, s[2] * kPScale, s[3] * kPScale, ph.x, pl.x);
-      pack4_fp8_split(s[4] * kPScale, s[5] * kPScale, s[6] * kPScale, s[7] * kPScale, ph.y, pl.y);
-      pack4_fp8_split(s[8] * kPScale, s[9] * kPScale, s[10] * kPScale, s[11] * kPScale, ph.z, pl.z);
-      pack4_fp8_split(s[12] * kPScale, s[13] * kPScale, s[14] * kPScale, s[15] * kPScale, ph.w, pl.w);
-      *reinterpret_cast<uint4*>(Pex + (g4 * 64 + lane) * 32 + 16 * half) = ph;
-      *reinterpret_cast<uint4*>(Pex + 8192 + (g4 * 64 + lane) * 32 + 16 * half) = pl;
-    }
+    l_run += psum * exp2f(dm);
+    // P'^T B operand: byte 16u + 4q + i <-> token 32u + 8q + 4hh + i; hi + lo fp8 terms
+    v8i pbh, pbl;
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) o[dt] *= alpha;
-    __syncthreads();  // (C) both halves of P visible
-    const v8i pbh = ld_v8(Pex + (g4 * 64 + lane) * 32);
-    const v8i pbl = ld_v8(Pex + 8192 + (g4 * 64 + lane) * 32);
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      const int d = 256 * half + 32 * dt + l32;
-      const int sw = vt128_sw(d);
-      v8i av;
-      {
-        const uint4 a0 = *reinterpret_cast<const uint4*>(Vt + d * 64 + 16 * ((2 * hh) ^ sw));
-        const uint4 a1 = *reinterpret_cast<const uint4*>(Vt + d * 64 + 16 * ((2 * hh + 1) ^ sw));
-        av[0] = a0.x; av[1] = a0.y; av[2] = a0.z; av[3] = a0.w;
-        av[4] = a1.x; av[5] = a1.y; av[6] = a1.z; av[7] = a1.w;
-      }
-      o[dt] = mfma32_f8(av, pbh, o[dt]);
-      o[dt] = mfma32_f8(av, pbl, o[dt]);
+    for (int q = 0; q < 4; ++q) {
+      uint32_t h0, l0, h1, l1;
+      pack4_fp8_split(s0[4 * q] * kPScale, s0[4 * q + 1] * kPScale, s0[4 * q + 2] * kPScale,
+                      s0[4 * q + 3] * kPScale, h0, l0);
+      pack4_fp8_split(s1[4 * q] * kPScale, s1[4 * q + 1] * kPScale, s1[4 * q + 2] * kPScale,
+                      s1[4 * q + 3] * kPScale, h1, l1);
+      pbh[q] = (int)h0;
+      pbl[q] = (int)l0;
+      pbh[4 + q] = (int)h1;
+      pbl[4 + q] = (int)l1;
     }
-    __syncthreads();  // (D) LDS free for the next tile
-  };
-  for (int ti = 0; ti + 1 < ntiles; ++ti) tile(std::true_type{}, ti);
-  if (ntiles > 0) tile(std::false_type{}, ntiles - 1);
+    // ---- O^T += V^T . P^T, V^T fragments by transpose reads of the row tile ------
+    auto vfrag = [&](int dt) -> v8i {
+      const uint32_t vb = lds0 + st * C::STAGE + 32 * dt;
+      const v2i r0 = lds_read_tr8(vb + tr_off[0]);
+      const v2i r1 = lds_read_tr8(vb + tr_off[1]);
+      const v2i r2 = lds_read_tr8(vb + tr_off[2]);
+      const v2i r3 = lds_read_tr8(vb + tr_off[3]);
+      return v8i{r0[0], r0[1], r1[0], r1[1], r2[0], r2[1], r3[0], r3[1]};
+    };
+    v8i avn = vfrag(0);
+#pragma unroll
+    for (int dt = 0; dt < 16; ++dt) {
+      const v8i av = avn;
+      if (dt < 15) avn = vfrag(dt + 1);
+      o[dt] = mfma32_f8_bscale(av, pbh, pscale, o[dt]);
+      o[dt] = mfma32_f8_bscale(av, pbl, pscale, o[dt]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  if (!restart && ntiles > 0) {
+    lds_barrier();  // the last tile's votes
+    restart = __builtin_amdgcn_readfirstlane(*reinterpret_cast<volatile uint32_t*>(vote + 4 * ((ntiles - 1) & 1))) != 0;
+  }
+  if (!restart) break;
+  // drain the ring (the prologue reuses it), then start over from m_ref = running max
+  wait_vmcnt<0>();
+  lds_barrier();
+  m_ref = m_seen;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) o[i] = v16f{};
+  l_run = 0.f;
+  }
 
-  // ---- finish: row sum over both lane halves and both half-waves ---------------
-  float l = l_run + shfl_xor_f(l_run, 32);
-  if (hh == 0) lsum[half * 128 + head] = l;
-  __syncthreads();
-  const float Lsum = lsum[head] + lsum[128 + head];
-  const float inv = Lsum > 0.f ? vscale / Lsum : 0.f;
+  // ---- finish ---------------------------------------------------------------------
+  const float L = l_run + shfl_xor_f(l_run, 32);
+  const float inv = L > 0.f ? vscale / L : 0.f;
   if (slot < 0) {
     uint16_t* orow = p.out + ((int64_t)b * 128 + head) * kVDim;
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
+    for (int dt = 0; dt < 16; ++dt) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int d = 256 * half + 32 * dt + 8 * q + 4 * hh;
+        const int d = 32 * dt + 8 * q + 4 * hh;
         const uint32_t lo = f32_to_bf16_bits(o[dt][4 * q] * inv) | (f32_to_bf16_bits(o[dt][4 * q + 1] * inv) << 16);
         const uint32_t hi = f32_to_bf16_bits(o[dt][4 * q + 2] * inv) | (f32_to_bf16_bits(o[dt][4 * q + 3] * inv) << 16);
         *reinterpret_cast<uint2*>(orow + d) = make_uint2(lo, hi);
       }
+      __builtin_amdgcn_sched_barrier(0);
     }
   } else {
     float* prow = p.part_o + ((int64_t)slot * 128 + head) * kVDim;
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
+    for (int dt = 0; dt < 16; ++dt) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int d = 256 * half + 32 * dt + 8 * q + 4 * hh;
+        const int d = 32 * dt + 8 * q + 4 * hh;
         *reinterpret_cast<float4*>(prow + d) = make_float4(o[dt][4 * q] * inv, o[dt][4 * q + 1] * inv,
                                                            o[dt][4 * q + 2] * inv, o[dt][4 * q + 3] * inv);
       }
+      __builtin_amdgcn_sched_barrier(0);
     }
-    if (hh == 0 && half == 0) p.part_lse[(int64_t)slot * 128 + head] = Lsum > 0.f ? m_run + __log2f(Lsum) : neg_inf();
+    if (hh == 0) p.part_lse[(int64_t)slot * 128 + head] = L > 0.f ? m_ref + __log2f(L) : neg_inf();
   }
 }
 
@@ -742,8 +860,8 @@ static hipError_t launch_decode_t(const DecodeParams& p, int kv_mode, int grid, 
     }
   } else if (p.num_heads == 128) {
     switch (kv_mode) {
-      case 0: hipLaunchKernelGGL((decode_h128_kernel<0, IDX>), dim3(grid), dim3(512), 0, stream, p); break;
-      case 2: hipLaunchKernelGGL((decode_h128_kernel<1, IDX>), dim3(grid), dim3(512), 0, stream, p); break;
+      case 0: hipLaunchKernelGGL((decode_h128_kernel<0, IDX>), dim3(grid), dim3(256), 0, stream, p); break;
+      case 2: hipLaunchKernelGGL((decode_h128_kernel<1, IDX>), dim3(grid), dim3(256), 0, stream, p); break;
       default: return hipErrorInvalidValue;
     }
   } else {

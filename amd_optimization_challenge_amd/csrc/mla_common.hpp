@@ -110,6 +110,10 @@ __device__ __forceinline__ v4f mfma16_f4f8(v8i a, int a_scale, v8i b, v4f c) {
 __device__ __forceinline__ v16f mfma32_f8(v8i a, v8i b, v16f c) {
   return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
 }
+// fp8 x fp8 with an e8m0 scale on B (one per lane: its column, 32 K values)
+__device__ __forceinline__ v16f mfma32_f8_bscale(v8i a, v8i b, int b_scale, v16f c) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 127, 0, b_scale);
+}
 __device__ __forceinline__ v16f mfma32_f4f8(v8i a, int a_scale, v8i b, v16f c) {
   return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 4, 0, 0, a_scale, 0, 127);
 }
@@ -127,6 +131,42 @@ __device__ __forceinline__ uint32_t pack4_fp8(float a, float b, float c, float d
   int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
   w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
   return (uint32_t)w;
+}
+
+// ---- LDS DMA (global_load_lds) and explicit waits --------------------------
+// The gfx950 LDS-DMA writes lane l's 16 (4) bytes to LDS at M0 + 16 l (4 l).
+// It is issued through inline asm so the compiler does not add conservative
+// vmcnt(0) waits before LDS reads and barriers: completion is tracked with
+// explicit wait_vmcnt<N>() calls, N = vector-memory ops issued after the one
+// that must have landed (vmcnt retires in order).  M0 is saved and restored.
+__device__ __forceinline__ void dma16_to_lds(const void* g, uint32_t lds_off) {
+  uint32_t tmp;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %2, off\n\ts_mov_b32 m0, %0"
+               : "=&s"(tmp)
+               : "s"(lds_off), "v"(g)
+               : "memory");
+}
+__device__ __forceinline__ void dma4_to_lds(const void* g, uint32_t lds_off) {
+  uint32_t tmp;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tglobal_load_lds_dword %2, off\n\ts_mov_b32 m0, %0"
+               : "=&s"(tmp)
+               : "s"(lds_off), "v"(g)
+               : "memory");
+}
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+// Work-group barrier for LDS only (no global-memory fence, so outstanding
+// DMA/prefetch loads are not drained).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// ds_read_b64_tr_b8: within each 16-lane group, result lane j gets byte (j & 7)
+// of the 8-byte reads of lanes 2m + (j >> 3), m = 0..7, in that order.
+typedef int v2i __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ v2i lds_read_tr8(uint32_t lds_off) {
+  typedef __attribute__((address_space(3))) v2i lds_v2i;
+  return __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(uintptr_t)lds_off);
 }
 
 // Byte-transpose of a 4x4 byte block: y[e] byte r = x[r] byte e.

@@ -268,6 +268,35 @@ __device__ void build_plan(const int32_t* __restrict__ kv_indptr, int batch, int
       binfo[b] = make_int2(rank, nb);  // rank for now; first item below
     }
     __syncthreads();
+    // exclusive scan of s_n in place, 256 at a time
+    for (int base = 0; base < batch; base += 256) {
+      const int i = base + tid;
+      const int v = i < batch ? s_n[i] : 0;
+      s_scan[tid] = v;
+      __syncthreads();
+      for (int off = 1; off < 256; off <<= 1) {
+        const int a = tid >= off ? s_scan[tid - off] : 0;
+        __syncthreads();
+        s_scan[tid] += a;
+        __syncthreads();
+      }
+      if (i < batch) s_n[i] = s_carry + s_scan[tid] - v;
+      __syncthreads();
+      if (tid == 255) s_carry += s_scan[255];
+      __syncthreads();
+    }
+    for (int b = tid; b < batch; b += 256) {
+      const int2 rb = binfo[b];  // written by this thread above
+      const int first = s_n[rb.x], nb = rb.y;
+      const int L = len_of(b);
+      const int s0 = kv_indptr[b];
+      binfo[b] = make_int2(first, nb);
+      for (int i = 0; i < nb; ++i) {
+        const int t0 = s0 + (int)(((long long)i * L) / nb);
+        const int t1 = s0 + (int)(((long long)(i + 1) * L) / nb);
+        items[first + i] = make_int4(b, t0, t1, nb > 1 ? first + i : -1);
+      }
+    }
   } else {
     for (int base = 0; base < batch; base += 256) {
       const int b = base + tid;

@@ -161,7 +161,38 @@ __global__ void fp4_probe_kernel(int big, float* __restrict__ out) {
   }
 }
 
+// LDS-DMA placement (13) and ds_read_b64_tr_b8 (14).  in: 1024 source bytes.
+// 13: lane l DMAs src[16*((7l) % 64) ..+16] to LDS offsets 0, 65536+1024 and
+//     131072+4096; out = the three 1 KiB LDS windows.
+// 14: LDS[i] = in[i % 1024] for i < 4096; lane l tr-reads at 8l (pattern A) and
+//     at 64(l % 8) + 8(l / 8) (pattern B); out = 64 x 8 bytes per pattern.
+__global__ void lds_probe_kernel(int which, const uint8_t* __restrict__ src, uint8_t* __restrict__ out) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[136192];
+  const int l = threadIdx.x;
+  const uint32_t base = (uint32_t)(uintptr_t)lds;
+  if (which == 13) {
+    const uint32_t offs[3] = {0u, 65536u + 1024u, 131072u + 4096u};
+    for (int k = 0; k < 3; ++k) dma16_to_lds(src + ((l * 7) % 64) * 16, base + offs[k]);
+    wait_vmcnt<0>();
+    __syncthreads();
+    for (int k = 0; k < 3; ++k)
+      for (int i = 0; i < 16; ++i) out[k * 1024 + l * 16 + i] = lds[offs[k] + l * 16 + i];
+  } else {
+    for (int i = l; i < 4096; i += 64) lds[i] = src[i % 1024];
+    __syncthreads();
+    const v2i a = lds_read_tr8(base + 8 * l);
+    const v2i b = lds_read_tr8(base + 64 * (l % 8) + 8 * (l / 8));
+    reinterpret_cast<v2i*>(out)[l] = a;
+    reinterpret_cast<v2i*>(out)[64 + l] = b;
+  }
+}
+
 hipError_t launch_selftest(int which, const void* in, void* out, hipStream_t stream) {
+  if (which == 13 || which == 14) {
+    hipLaunchKernelGGL(lds_probe_kernel, dim3(1), dim3(64), 0, stream, which,
+                       static_cast<const uint8_t*>(in), static_cast<uint8_t*>(out));
+    return hipGetLastError();
+  }
   if (which == 11 || which == 12) {
     hipLaunchKernelGGL(fp4_probe_kernel, dim3(1), dim3(64), 0, stream, which == 12 ? 1 : 0,
                        static_cast<float*>(out));

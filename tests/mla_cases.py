@@ -13,6 +13,11 @@ TOL = 2e-2  # north-star tolerance on the bf16 output: atol = rtol = 2e-2
 
 def host_case(lens, heads, kv_mode, seed, permute=True):
     q, kv, indptr, idx = inputs.make_host_inputs(len(lens), heads, ("list", lens), seed, permute)
+    return case_from_tensors(q, kv, indptr, idx, kv_mode)
+
+
+def case_from_tensors(q, kv, indptr, idx, kv_mode):
+    """Oracle caches (bit-exact quantizers) for given bf16 q [B,H,576] / kv [T,1,576]."""
     qb = O.bf16_tensor_bits(q)
     kvb = O.bf16_tensor_bits(kv).reshape(-1, 576)
     caches = {}
@@ -44,7 +49,11 @@ def device_data(q, kv, indptr, idx, caches, kv_mode, sm_scale, pass_indices=True
 
 
 def run_and_reference(lens, heads, kv_mode, seed=0, sm_scale=1 / math.sqrt(192), permute=True):
-    q, kv, indptr, idx, qb, caches = host_case(lens, heads, kv_mode, seed, permute)
+    return run_case(host_case(lens, heads, kv_mode, seed, permute), kv_mode, sm_scale)
+
+
+def run_case(case, kv_mode, sm_scale):
+    q, kv, indptr, idx, qb, caches = case
     data = device_data(q, kv, indptr, idx, caches, kv_mode, sm_scale)
     out = custom_kernel(data)
     torch.cuda.synchronize()

@@ -7,7 +7,7 @@ import pytest
 import torch
 
 from amd_optimization_challenge_amd import custom_kernel
-from mla_cases import assert_close, device_data, host_case, run_and_reference
+from mla_cases import assert_close, case_from_tensors, device_data, host_case, run_and_reference, run_case
 
 pytestmark = pytest.mark.gpu
 
@@ -39,6 +39,31 @@ def test_sm_scale_is_honoured(cuda, heads, mode):
     for sm in (1 / math.sqrt(576), 0.3):
         got, ref, _ = run_and_reference([300, 77], heads, mode, seed=5, sm_scale=sm)
         assert_close(got, ref)
+
+
+@pytest.mark.parametrize("heads,mode", MODES)
+def test_wide_score_range(cuda, heads, mode):
+    """Scores that climb by ~100 (log2 units) per 64-token tile: far beyond the
+    fp8 range of P, so every tile needs its own offset (and, for H=128, the
+    accumulator reference restarts)."""
+    print(f"wide score range H={heads} mode={mode}", flush=True)
+    g = torch.Generator().manual_seed(17)
+    lens = [700, 130, 5]
+    T = sum(lens)
+    q = torch.randn(len(lens), heads, 576, generator=g)
+    q[..., 7] = 40.0
+    kv = 0.25 * torch.randn(T, 1, 576, generator=g)
+    pos = torch.cat([torch.arange(L) for L in lens]).float()
+    kv[:, 0, 7] = 6.0 * torch.floor(pos / 64) - 20.0 + 0.1 * torch.randn(T, generator=g)
+    indptr = torch.tensor([0] + list(np.cumsum(lens)), dtype=torch.int32)
+    idx = torch.randperm(T, generator=g).to(torch.int32)
+    # kv rows are addressed through idx: place token j of the flattened sequences at row idx[j]
+    rows = torch.empty_like(kv)
+    rows[idx.long()] = kv
+    case = case_from_tensors(q.to(torch.bfloat16), rows.to(torch.bfloat16), indptr, idx, mode)
+    got, ref, _ = run_case(case, mode, 1 / math.sqrt(192))
+    assert np.all(np.isfinite(got))
+    assert_close(got, ref)
 
 
 @pytest.mark.parametrize("heads,mode", [(16, "fp8"), (128, "fp8"), (16, "mxfp4")])

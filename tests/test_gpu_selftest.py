@@ -11,7 +11,7 @@ pytestmark = pytest.mark.gpu
 
 
 IN_BYTES = {0: 4096, 1: 4096, 2: 3136, 3: 3136, 4: 1024, 5: 2048, 6: 1024, 7: 512, 8: 1024, 9: 1024,
-            10: 256, 11: 0, 12: 0}
+            10: 256, 11: 0, 12: 0, 13: 1024, 14: 1024}
 
 
 def run(which, inp: np.ndarray, out_bytes: int) -> np.ndarray:
@@ -155,3 +155,27 @@ def test_fp4_operand_k_map(cuda, which, npos):
     got = run(which, np.zeros(16, np.uint8), npos * 8 * 4).view(np.float32).reshape(npos, 8)
     kmap = (got[:, :7] > 0.5).astype(int) @ (1 << np.arange(7))
     assert np.array_equal(kmap, expected_kmap(npos)), kmap.tolist()
+
+
+def test_lds_dma_lane_placement(cuda):
+    """global_load_lds_dwordx4: lane l's 16 bytes land at M0 + 16 l, also above 64 KiB."""
+    src = (np.arange(1024) * 13 + 5).astype(np.uint8)
+    got = run(13, src, 3 * 1024).reshape(3, 64, 16)
+    exp = src.reshape(64, 16)[(np.arange(64) * 7) % 64]
+    for k in range(3):
+        assert np.array_equal(got[k], exp), k
+
+
+def test_lds_transpose_read_b8(cuda):
+    """ds_read_b64_tr_b8: lane j of each 16-lane group gets byte j&7 of lanes 2m + (j>>3)."""
+    src = np.random.default_rng(14).integers(0, 256, 1024, dtype=np.uint8)
+    lds = np.resize(src, 4096)
+    got = run(14, src, 2 * 64 * 8).reshape(2, 64, 8)
+    for pat, addr in enumerate([8 * np.arange(64), 64 * (np.arange(64) % 8) + 8 * (np.arange(64) // 8)]):
+        rows = np.stack([lds[a:a + 8] for a in addr])  # what each lane's plain 8-byte read would return
+        exp = np.empty((64, 8), np.uint8)
+        for l in range(64):
+            g, j = l // 16, l % 16
+            for m in range(8):
+                exp[l, m] = rows[16 * g + 2 * m + (j >> 3), j & 7]
+        assert np.array_equal(got[pat], exp), pat
