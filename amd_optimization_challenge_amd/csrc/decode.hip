@@ -68,138 +68,6 @@ __device__ __forceinline__ float e8m0_to_f32(uint32_t e) {
   return e == 0 ? __uint_as_float(0x00400000u) : __uint_as_float(e << 23);
 }
 
-// ============================================================================
-// Tile loader: one 64-token tile of cache rows gathered through kv_indices.
-// Thread t serves token quad tq = t / QPT (tokens 4tq .. 4tq+3) and the 16-byte
-// chunks ch = t % QPT + QPT*j of those four rows, so it needs four slot indices
-// per tile; they are fetched one tile ahead of the rows.  Row loads never wait
-// on each other: a token past the end of the item reads slot 0 and is zeroed
-// when the registers are written to LDS (after the loads have landed).
-// ============================================================================
-template <int NT, int KF, int VF, bool IDX>
-struct TileLoader {
-  static constexpr int QPT = NT / 16;
-  static constexpr int KCH = KF == 0 ? 36 : 18;
-  static constexpr int KJ = (KCH + QPT - 1) / QPT;
-  static constexpr int VJ = VF == 1 ? (32 + QPT - 1) / QPT : 1;
-  static constexpr int SJ = KF == 1 ? (kMxBlocks + QPT - 1) / QPT : 1;
-
-  int tq, lq;
-  int sl_nxt[4];       // cache slots of the quad's tokens for the next tile to load
-  int vmask;           // bit r set: token 4tq+r of the loaded tile is valid
-  uint4 kr[KJ][4];
-  uint4 vr[VJ][4];
-  uint32_t sr[SJ][4];  // e8m0 of block lq + QPT*j for the quad's 4 tokens
-
-  __device__ __forceinline__ void init(int tid) {
-    tq = tid / QPT;
-    lq = tid - tq * QPT;
-  }
-  // Slots of tokens pos0 + 4tq + r, r < 4.  Positions are clamped to last
-  // (a valid position), so the loads are unconditional and their results are
-  // only consumed when the rows are gathered, a tile later.
-  __device__ __forceinline__ void load_idx(const DecodeParams& p, int pos0, int last, int (&sl)[4]) const {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int pos = min(pos0 + 4 * tq + r, last);
-      if constexpr (IDX) sl[r] = p.kv_indices[pos];
-      else sl[r] = pos;
-    }
-  }
-  __device__ __forceinline__ void load_rows(const DecodeParams& p, const int (&sl)[4], int nval) {
-    vmask = 0;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) vmask |= (4 * tq + r < nval ? 1 : 0) << r;
-#pragma unroll
-    for (int j = 0; j < KJ; ++j) {
-      const int ch = min(lq + QPT * j, KCH - 1);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) kr[j][r] = ldg16(p.k_cache + (int64_t)sl[r] * p.k_row_stride + 16 * ch);
-    }
-    if constexpr (VF == 1) {
-#pragma unroll
-      for (int j = 0; j < VJ; ++j) {
-        const int ch = min(lq + QPT * j, 31);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) vr[j][r] = ldg16(p.v_cache + (int64_t)sl[r] * p.v_row_stride + 16 * ch);
-      }
-    }
-    if constexpr (KF == 1) {
-#pragma unroll
-      for (int j = 0; j < SJ; ++j) {
-        const int blk = min(lq + QPT * j, kMxBlocks - 1);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) sr[j][r] = p.k_scales[(int64_t)sl[r] * p.k_scale_stride + blk];
-      }
-    }
-  }
-  __device__ __forceinline__ bool valid(int r) const { return (vmask >> r) & 1; }
-  __device__ __forceinline__ uint4 kget(int j, int r) const { return valid(r) ? kr[j][r] : make_uint4(0, 0, 0, 0); }
-  __device__ __forceinline__ uint4 vget(int j, int r) const { return valid(r) ? vr[j][r] : make_uint4(0, 0, 0, 0); }
-
-  // row-major K tile (+ e8m0 scales for fp4 K)
-  __device__ __forceinline__ void store_k(uint8_t* Klds, int kst, uint8_t* Slds) const {
-#pragma unroll
-    for (int j = 0; j < KJ; ++j) {
-      const int ch = lq + QPT * j;
-      if (ch < KCH) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) *reinterpret_cast<uint4*>(Klds + (4 * tq + r) * kst + 16 * ch) = kget(j, r);
-      }
-    }
-    if constexpr (KF == 1) {
-#pragma unroll
-      for (int j = 0; j < SJ; ++j) {
-        const int blk = lq + QPT * j;
-        if (blk < kMxBlocks) {
-#pragma unroll
-          for (int r = 0; r < 4; ++r) Slds[(4 * tq + r) * 20 + blk] = valid(r) ? (uint8_t)sr[j][r] : (uint8_t)127;
-        }
-      }
-    }
-  }
-  // fp8 V^T: for each latent dim of chunk ch, the quad's four bytes as one word
-  template <class Off>
-  __device__ __forceinline__ void store_vt_fp8(uint8_t* Vt, const uint4 (&x)[4], int ch, Off off) const {
-    const uint32_t* x0 = reinterpret_cast<const uint32_t*>(&x[0]);
-    const uint32_t* x1 = reinterpret_cast<const uint32_t*>(&x[1]);
-    const uint32_t* x2 = reinterpret_cast<const uint32_t*>(&x[2]);
-    const uint32_t* x3 = reinterpret_cast<const uint32_t*>(&x[3]);
-#pragma unroll
-    for (int wd = 0; wd < 4; ++wd) {
-      uint32_t y[4];
-      transpose4x4_bytes(x0[wd], x1[wd], x2[wd], x3[wd], y);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int d = 16 * ch + 4 * wd + e;
-        *reinterpret_cast<uint32_t*>(Vt + off(d, tq)) = y[e];
-      }
-    }
-  }
-  template <class Off>
-  __device__ __forceinline__ void store_v_fp8(uint8_t* Vt, Off off) const {
-    if constexpr (VF == 0) {
-#pragma unroll
-      for (int j = 0; j < KJ; ++j) {
-        const int ch = lq + QPT * j;
-        if (ch < 32) {
-          uint4 x[4] = {kget(j, 0), kget(j, 1), kget(j, 2), kget(j, 3)};
-          store_vt_fp8(Vt, x, ch, off);
-        }
-      }
-    } else if constexpr (VF == 1) {
-#pragma unroll
-      for (int j = 0; j < VJ; ++j) {
-        const int ch = lq + QPT * j;
-        if (ch < 32) {
-          uint4 x[4] = {vget(j, 0), vget(j, 1), vget(j, 2), vget(j, 3)};
-          store_vt_fp8(Vt, x, ch, off);
-        }
-      }
-    }
-  }
-};
-
 // Two-term fp8 encoding of four non-negative values (< 448): hi = e4m3(x),
 // lo = e4m3(x - hi).  hi + lo carries ~7 significant bits; both terms enter
 // the same MFMA accumulator.
@@ -211,54 +79,81 @@ __device__ __forceinline__ void pack4_fp8_split(float a, float b, float c, float
   lo = pack4_fp8(a - h01[0], b - h01[1], c - h23[0], d - h23[1]);
 }
 
+// waits until at most k groups of PER operations issued after the one waited
+// for are still outstanding (k in 0..2, the ring depth minus two)
+template <int PER>
+__device__ __forceinline__ void wait_groups(int k) {
+  if (k <= 0) wait_vmcnt<0>();
+  else if (k == 1) wait_vmcnt<PER>();
+  else wait_vmcnt<2 * PER>();
+}
+
 // ============================================================================
-// H = 16
+// H = 16.  4 waves; per 64-token tile wave w scores 16 tokens for all 16
+// heads (16x16x128 MFMAs, Q^T in registers) and accumulates O^T for latent
+// dims 128w .. 128w+127 over all 64 tokens.  Cache rows arrive by LDS-DMA in
+// an S-stage ring (slots one tile ahead of the rows they address).
 //   KF: 0 = fp8 K rows (576 B), 1 = packed fp4 K rows (288 B) + e8m0 scales
 //   VF: 0 = fp8 V = K rows, 1 = fp8 V from its own cache, 2 = fp4 V = K rows
+// fp8 V: P^T enters a block-scaled 16x16x128 MFMA as two fp8 terms whose e8m0
+// B scale carries 2^(m_w - m_ref - 8): m_w is the wave's own (ceil) max for the
+// head, m_ref a per-item reference, so no cross-wave max and no rescale of
+// O^T per tile.  The A operand (V^T) comes from the row-major tile through
+// ds_read_b64_tr_b8; K block g of the MFMA holds wave g's 16 tokens (+16 zeros).
+// fp4 V: the tile is dequantized to a bf16 V^T in LDS and P = 2^(s - m_ref) is
+// bf16; PV runs on 16x16x32 bf16 MFMAs.
+// A tile max more than kRebase above m_ref restarts the item from a higher
+// reference (block-wide vote), so the accumulators cannot overflow.
 // ============================================================================
 template <int KF, int VF>
 struct H16 {
   static constexpr int KROW = KF == 0 ? 576 : 288;
-  static constexpr int KST = KROW + 16;               // LDS row stride (bank spread)
-  static constexpr bool VB16 = VF == 2;               // V^T / P held as bf16
-  static constexpr int VTST = VB16 ? 144 : 72;        // LDS bytes per latent-dim row of V^T
-  static constexpr int PST = VB16 ? 144 : 72;
-  static constexpr int NPLANE = VB16 ? 1 : 2;         // fp8 P: hi and lo planes
-  static constexpr int OFF_K = 0;
-  static constexpr int OFF_S = OFF_K + kTile * KST;
-  static constexpr int OFF_VT = OFF_S + (KF == 1 ? kTile * 20 : 0);
-  static constexpr int OFF_P = OFF_VT + kVDim * VTST;
-  static constexpr int OFF_MAX = OFF_P + NPLANE * 16 * PST;
-  static constexpr int OFF_L = OFF_MAX + 4 * 16 * 4;
-  static constexpr int LDS = OFF_L + 4 * 16 * 4;
+  static constexpr int KST = KROW + 16;                        // LDS row stride: 592 / 304
+  static constexpr int KCPR = KST / 16;                        // 16-B chunks per LDS row: 37 / 19
+  static constexpr int KCH = KROW / 16;                        // real chunks: 36 / 18
+  static constexpr int VST = 528, VCPR = 33;                   // fp8 V rows (VF == 1): 512 B used
+  static constexpr int KW = kTile * KST / 1024;                // 1-KiB DMA windows of K rows: 37 / 19
+  static constexpr int VW = VF == 1 ? kTile * VST / 1024 : 0;  // of V rows: 33
+  static constexpr int NW = KW + VW;
+  static constexpr int STAGE = NW * 1024;
+  static constexpr int S = KF == 0 ? 4 : (VF == 1 ? 2 : 3);      // ring depth (tiles)
+  static constexpr int RW0 = KF == 1 ? 1 : 0;                  // waves RW0..3 DMA rows; wave 0 the scales
+  static constexpr int NRW = 4 - RW0;
+  static constexpr int NA = (NW + NRW - 1) / NRW;              // windows per row wave: NA or NA - 1
+  static constexpr int NAW = NW % NRW == 0 ? NRW : NW % NRW;   // row waves (from RW0) that issue NA
+  static constexpr bool VB16 = VF == 2;
+  static constexpr int VTST = 144;                             // bf16 V^T / P^T row stride
+  static constexpr int NSL = 2 * S;                            // slot stages (slots lead rows by S - 1 tiles)
+  static constexpr int OFF_SLOT = S * STAGE;                   // [NSL][64] int32 cache slots
+  static constexpr int SCST = kMxBlocks * 256;                 // e8m0 stage: [18 blocks][64 tokens] dwords
+  static constexpr int OFF_SC = OFF_SLOT + NSL * 256;          // [S] e8m0 stages (KF == 1)
+  static constexpr int OFF_VT = OFF_SC + (KF == 1 ? S * SCST : 0);
+  static constexpr int OFF_P = OFF_VT + (VB16 ? kVDim * VTST : 0);
+  static constexpr int P_BYTES = VB16 ? 16 * VTST : 2 * 4 * 16 * 16;  // bf16 [h][pos] | fp8 [term][g][h][16]
+  static constexpr int OFF_PS = OFF_P + P_BYTES;               // [g][h] e8m0 B scales
+  static constexpr int OFF_X = OFF_PS + 64;                    // [4][16] f32 exchange
+  static constexpr int OFF_VOTE = OFF_X + 256;
+  static constexpr int LDS = OFF_VOTE + 16;
 };
-
-// fp8 V^T row of latent dim d holds 64 tokens in natural order as eight 8-byte
-// chunks; chunk c is stored at c ^ ((d >> 4) & 7) to spread the transposed
-// writes of 16 consecutive chunks over the banks.
-__device__ __forceinline__ int vt16_quad_off(int d, int tq) {
-  return d * 72 + 8 * ((tq >> 1) ^ ((d >> 4) & 7)) + 4 * (tq & 1);
-}
-__device__ __forceinline__ int vt16_read_off(int d, int chunk8) { return d * 72 + 8 * (chunk8 ^ ((d >> 4) & 7)); }
 
 template <int KF, int VF, bool IDX>
 __global__ __launch_bounds__(256, 1) void decode_h16_kernel(const DecodeParams p) {
   using C = H16<KF, VF>;
-  __shared__ __attribute__((aligned(16))) uint8_t smem[C::LDS];
-  uint8_t* Klds = smem + C::OFF_K;
-  uint8_t* Slds = smem + C::OFF_S;
-  uint8_t* Vt = smem + C::OFF_VT;
-  uint8_t* Pl = smem + C::OFF_P;
-  float* wmax = reinterpret_cast<float*>(smem + C::OFF_MAX);
-  float* lsum = reinterpret_cast<float*>(smem + C::OFF_L);
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[C::LDS];
+  const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
 
   const int32_t* plan = p.plan;
   if ((int)blockIdx.x >= plan[0]) return;
   const int4 it = reinterpret_cast<const int4*>(plan + kPlanHeader)[blockIdx.x];
   const int b = it.x, t_beg = it.y, t_end = it.z, slot = it.w;
+  const int ntok = t_end - t_beg;
+  const int ntiles = (ntok + kTile - 1) / kTile;
 
   const int tid = threadIdx.x;
-  const int w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (feeds M0)
+  const int lane = tid & 63, l16 = lane & 15, g = lane >> 4;
+
+  auto tok_of = [](int gg, int i) { return 16 * gg + i; };  // tile token of row i of wave gg's slice
 
   // ---- Q^T (B operand): head l16, dims 128ks + 32g .. +31 -------------------
   // With fp4 K, the f8f6f4 MFMA pairs fp4 element e of lane group g (K =
@@ -287,168 +182,284 @@ __global__ __launch_bounds__(256, 1) void decode_h16_kernel(const DecodeParams p
   const float qs = p.q_scale[0];
   const float kvs = (KF == 0 || VF == 1) ? p.kv_scale[0] : 1.0f;
   const float c = qs * (KF == 0 ? kvs : 1.0f) * p.sm_scale * kLog2e;
-  const float vscale = (VF == 2 ? 1.0f : kvs / kPScale);
+  const float vscale = VF == 2 ? 1.0f : kvs;
 
   v4f o[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) o[i] = v4f{0.f, 0.f, 0.f, 0.f};
-  float m_run = neg_inf(), l_run = 0.f;
+  float m_ref = 0.f, m_seen = neg_inf(), l_part = 0.f;
+  bool have_ref = false;
 
-  TileLoader<256, KF, VF, IDX> L;
-  L.init(tid);
-  auto vt_off = [](int d, int tq) { return vt16_quad_off(d, tq); };
+  // ---- ring issue ----------------------------------------------------------
+  // slots of tile t live in slot stage t % NSL
+  auto slot_of = [&](int t, int tok) -> int {
+    if constexpr (IDX) return reinterpret_cast<const int*>(smem + C::OFF_SLOT + (t % C::NSL) * 256)[tok];
+    else return min(t_beg + kTile * t + tok, t_end - 1);
+  };
+  auto issue_slots = [&](int t) {  // wave 0: the 64 slots of tile t (positions clamped into the item)
+    if constexpr (IDX) {
+      if (w == 0) {
+        const int pos = min(t_beg + kTile * t + lane, t_end - 1);
+        dma4_to_lds(p.kv_indices + pos, lds0 + C::OFF_SLOT + (t % C::NSL) * 256);
+      }
+    }
+  };
+  auto issue_rows = [&](int t) {  // row waves: windows u = (w - RW0) + NRW k of tile t
+    if (w < C::RW0) return;
+    const int st = t % C::S;
+    const uint32_t sbase = lds0 + st * C::STAGE;
+#pragma unroll
+    for (int k = 0; k < C::NA; ++k) {
+      const int u = (w - C::RW0) + C::NRW * k;
+      if (u < C::NW) {
+        const uint8_t* src;
+        if (u < C::KW) {
+          const int e = 64 * u + lane;  // 16-B chunk index within the stage
+          const int tok = e / C::KCPR, ch = e - tok * C::KCPR;
+          src = p.k_cache + (int64_t)slot_of(t, tok) * p.k_row_stride + 16 * min(ch, C::KCH - 1);
+        } else {
+          const int e = 64 * (u - C::KW) + lane;
+          const int tok = e / C::VCPR, ch = e - tok * C::VCPR;
+          src = p.v_cache + (int64_t)slot_of(t, tok) * p.v_row_stride + 16 * min(ch, 31);
+        }
+        dma16_to_lds(src, sbase + 1024 * u);
+      }
+    }
+  };
+  // fp4 K scales: wave 0 DMAs the 18 e8m0 bytes of token `lane` of tile t, one
+  // byte per lane and instruction; byte j lands in dword j * 64 + lane of the
+  // tile's scale stage (sub-dword LDS-DMA writes one dword per lane)
+  auto issue_scales = [&](int t) {
+    if constexpr (KF == 1) {
+      if (w == 0) {
+        const uint8_t* srow = p.k_scales + (int64_t)slot_of(t, lane) * p.k_scale_stride;
+        const uint32_t sb = lds0 + C::OFF_SC + (t % C::S) * C::SCST;
+#pragma unroll
+        for (int j = 0; j < kMxBlocks; ++j) dma1_to_lds(srow + j, sb + 256 * j);
+      }
+    }
+  };
+  // this wave's wait for tile t's rows (and scales), k groups issued after them
+  auto wait_tile = [&](int k) {
+    if constexpr (KF == 1) {
+      constexpr int SL = IDX ? 1 : 0;  // wave 0: one slot DMA + 18 scale DMAs per group
+      if (w == 0) wait_groups<kMxBlocks + SL>(k);
+      else if (w - C::RW0 < C::NAW) wait_groups<C::NA>(k);
+      else wait_groups<C::NA - 1>(k);
+    } else {
+      constexpr int SL = IDX ? 1 : 0;  // wave 0 issues one slot DMA per group
+      if (w == 0) wait_groups<C::NA + SL>(k);
+      else if (w < C::NAW) wait_groups<C::NA>(k);
+      else wait_groups<C::NA - 1>(k);
+    }
+  };
+  // group x = {slots(x + S - 1), rows(x) | scales(x)}, issued S - 1 tiles
+  // ahead of the tile x compute: once a group has landed, so have the slots
+  // the rows of group x + S - 1 need
+  auto prologue = [&]() {
+#pragma unroll
+    for (int j = 0; j < C::S - 1; ++j) issue_slots(j);
+    wait_vmcnt<0>();
+    lds_barrier();
+#pragma unroll
+    for (int j = 0; j < C::S - 1; ++j) {
+      if (j >= ntiles) break;
+      issue_slots(j + C::S - 1);
+      issue_rows(j);
+      issue_scales(j);
+    }
+  };
 
-  const int ntok = t_end - t_beg;
-  const int ntiles = (ntok + kTile - 1) / kTile;
-  const int last = t_end - 1;
-  if (ntiles > 0) {
-    int sl[4];
-    L.load_idx(p, t_beg, last, sl);
-    L.load_rows(p, sl, min(kTile, ntok));
-    L.load_idx(p, t_beg + kTile, last, L.sl_nxt);
-  }
+  // ---- main loop ---------------------------------------------------------------
+  int8_t* vote = reinterpret_cast<int8_t*>(smem + C::OFF_VOTE);
+  float* xch = reinterpret_cast<float*>(smem + C::OFF_X);
+  for (;;) {
+    bool restart = false;
+    if (ntiles > 0) prologue();
+    for (int ti = 0; ti < ntiles; ++ti) {
+      const int st = ti % C::S;
+      const int nval = min(kTile, ntok - kTile * ti);
+      wait_tile(min(C::S - 2, ntiles - 1 - ti));
+      lds_barrier();  // (1) tile ti and its scales visible; iteration ti-1 done everywhere
+      if (ti + C::S - 1 < ntiles) {
+        issue_slots(ti + 2 * C::S - 2);
+        issue_rows(ti + C::S - 1);
+        issue_scales(ti + C::S - 1);
+      }
+      const uint8_t* kt = smem + st * C::STAGE;
+      const uint8_t* sct = smem + C::OFF_SC + st * C::SCST;  // e8m0 of (token t, block j) at 256 j + 4 t
 
-  // one 64-token tile; PF: prefetch the next tile's rows and the slots of the one after
-  auto tile = [&](auto pf, int ti) {
-    constexpr bool PF = decltype(pf)::value;
-    const int t0 = ti * kTile;
-    const int nval = min(kTile, ntok - t0);
-    // ---- registers -> LDS ------------------------------------------------------
-    L.store_k(Klds, C::KST, Slds);
-    if constexpr (VF == 2) {
-      // fp4 V: chunk lq (latent dims 32lq .. +31, scale block lq) -> bf16 V^T
-      const int ch = L.lq;
-      float sc[4];
+      // ---- scores: rows i = l16 of this wave's slice, 16x16x128 MFMAs ----------
+      v4f s = v4f{0.f, 0.f, 0.f, 0.f};
+      {
+        const uint8_t* kp = kt + tok_of(w, l16) * C::KST;
+        if constexpr (KF == 0) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) sc[r] = e8m0_to_f32(L.valid(r) ? L.sr[0][r] : 127u);
+          for (int ks = 0; ks < 4; ++ks) s = mfma16_f8(ld_v8(kp + 128 * ks + 32 * g), qv[ks], s);
+          const v8i a4 = g < 2 ? ld_v8(kp + 512 + 32 * g) : v8i{0, 0, 0, 0, 0, 0, 0, 0};
+          s = mfma16_f8(a4, qv[4], s);
+        } else {
+          const uint8_t* sp = sct + 4 * tok_of(w, l16);
 #pragma unroll
-      for (int wd = 0; wd < 4; ++wd) {
-        uint32_t xw[4];
+          for (int ks = 0; ks < 5; ++ks) {
+            const int blk = 4 * ks + g;
+            const v8i a = blk < kMxBlocks ? ld_v4_as_v8(kp + 16 * blk) : v8i{0, 0, 0, 0, 0, 0, 0, 0};
+            const int sc = blk < kMxBlocks ? (int)sp[256 * blk] : 127;
+            s = mfma16_f4f8(a, sc, qv[ks], s);
+          }
+        }
+      }
+      // s[r] = score(token tok_of(w, 4g + r), head l16)
+      float sv[4];
+      float mx = neg_inf();
 #pragma unroll
-        for (int r = 0; r < 4; ++r) xw[r] = reinterpret_cast<const uint32_t*>(&L.kr[0][r])[wd] & (L.valid(r) ? 0xFFFFFFFFu : 0u);
-        uint32_t bf[4][4];  // [token][byte] -> bf16 pair (dims 2k, 2k+1)
+      for (int r = 0; r < 4; ++r) {
+        sv[r] = tok_of(w, 4 * g + r) < nval ? s[r] * c : neg_inf();
+        mx = fmaxf(mx, sv[r]);
+      }
+      mx = fmaxf(mx, shfl_xor_f(mx, 16));
+      mx = fmaxf(mx, shfl_xor_f(mx, 32));
+      const float m_w = mx == neg_inf() ? neg_inf() : __builtin_ceilf(mx);
+      m_seen = fmaxf(m_seen, m_w);
+      if (!have_ref) {  // first tile of the first pass: m_ref = tile max over the waves
+        if (g == 0) xch[16 * w + l16] = m_w;
+        lds_barrier();
+        m_ref = fmaxf(fmaxf(xch[l16], xch[16 + l16]), fmaxf(xch[32 + l16], xch[48 + l16]));
+        have_ref = true;
+      }
+      const bool over = __any(m_w > m_ref + kRebase);
+      if (lane == 0) vote[w] = over ? 1 : 0;
+
+      if constexpr (!C::VB16) {
+        // P' = 2^(s - m_w) * 2^8 (two fp8 terms); B scale 2^(m_w - m_ref - 8)
+        const float mw = m_w == neg_inf() ? m_ref : m_w;
+        const float dm = fminf(fmaxf(mw - m_ref, -160.f), 160.f);
+        float pv[4], ps = 0.f;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          bf[r][0] = cvt_fp4_byte<0>(xw[r], sc[r]);
-          bf[r][1] = cvt_fp4_byte<1>(xw[r], sc[r]);
-          bf[r][2] = cvt_fp4_byte<2>(xw[r], sc[r]);
-          bf[r][3] = cvt_fp4_byte<3>(xw[r], sc[r]);
+          pv[r] = __builtin_amdgcn_exp2f(sv[r] - mw);
+          ps += pv[r];
         }
+        l_part += ps * __builtin_amdgcn_exp2f(dm);
+        uint32_t hi, lo;
+        pack4_fp8_split(pv[0] * kPScale, pv[1] * kPScale, pv[2] * kPScale, pv[3] * kPScale, hi, lo);
+        uint8_t* pl = smem + C::OFF_P + w * 256 + l16 * 16 + 4 * g;
+        *reinterpret_cast<uint32_t*>(pl) = hi;
+        *reinterpret_cast<uint32_t*>(pl + 4 * 256) = lo;
+        if (g == 0) smem[C::OFF_PS + 16 * w + l16] = (uint8_t)min(max((int)dm - 8 + 127, 0), 254);
+      } else {
+        // bf16 P = 2^(s - m_ref) at V^T position 4 i + w of token 16 w + i
+        uint16_t* prow = reinterpret_cast<uint16_t*>(smem + C::OFF_P + l16 * C::VTST);
 #pragma unroll
-        for (int bt = 0; bt < 4; ++bt) {
-          const int d0 = 32 * ch + 8 * wd + 2 * bt;
-          const uint2 ev = make_uint2(__builtin_amdgcn_perm(bf[1][bt], bf[0][bt], 0x05040100u),
-                                      __builtin_amdgcn_perm(bf[3][bt], bf[2][bt], 0x05040100u));
-          const uint2 od = make_uint2(__builtin_amdgcn_perm(bf[1][bt], bf[0][bt], 0x07060302u),
-                                      __builtin_amdgcn_perm(bf[3][bt], bf[2][bt], 0x07060302u));
-          *reinterpret_cast<uint2*>(Vt + d0 * C::VTST + 8 * L.tq) = ev;
-          *reinterpret_cast<uint2*>(Vt + (d0 + 1) * C::VTST + 8 * L.tq) = od;
+        for (int r = 0; r < 4; ++r) {
+          const uint32_t pb = f32_to_bf16_bits(__builtin_amdgcn_exp2f(fminf(sv[r] - m_ref, 120.f)));
+          l_part += __uint_as_float(pb << 16);
+          prow[4 * (4 * g + r) + w] = (uint16_t)pb;
+        }
+        // fp4 V -> bf16 V^T: thread (tokens di + 16 r, MX block dc); token
+        // di + 16 r lands at position 4 di + r of latent-dim row d
+        const int di = tid & 15, dc = tid >> 4;
+        uint4 raw[4];
+        float scv[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          raw[r] = *reinterpret_cast<const uint4*>(kt + (di + 16 * r) * C::KST + 16 * dc);
+          scv[r] = e8m0_to_f32(sct[256 * dc + 4 * (di + 16 * r)]);
+        }
+        uint8_t* vt = smem + C::OFF_VT;
+#pragma unroll
+        for (int wd = 0; wd < 4; ++wd) {
+          uint32_t bf[4][4];  // [token r][byte bt] -> bf16 pair (dims 2bt, 2bt+1 of the word)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const uint32_t xw = reinterpret_cast<const uint32_t*>(&raw[r])[wd];
+            bf[r][0] = cvt_fp4_byte<0>(xw, scv[r]);
+            bf[r][1] = cvt_fp4_byte<1>(xw, scv[r]);
+            bf[r][2] = cvt_fp4_byte<2>(xw, scv[r]);
+            bf[r][3] = cvt_fp4_byte<3>(xw, scv[r]);
+          }
+#pragma unroll
+          for (int bt = 0; bt < 4; ++bt) {
+            const int d0 = 32 * dc + 8 * wd + 2 * bt;
+            const uint2 ev = make_uint2(__builtin_amdgcn_perm(bf[1][bt], bf[0][bt], 0x05040100u),
+                                        __builtin_amdgcn_perm(bf[3][bt], bf[2][bt], 0x05040100u));
+            const uint2 od = make_uint2(__builtin_amdgcn_perm(bf[1][bt], bf[0][bt], 0x07060302u),
+                                        __builtin_amdgcn_perm(bf[3][bt], bf[2][bt], 0x07060302u));
+            *reinterpret_cast<uint2*>(vt + d0 * C::VTST + 8 * di) = ev;
+            *reinterpret_cast<uint2*>(vt + (d0 + 1) * C::VTST + 8 * di) = od;
+          }
         }
       }
-    } else {
-      L.store_v_fp8(Vt, vt_off);
-    }
-    __syncthreads();  // (A) tile visible
-    if constexpr (PF) {
-      L.load_rows(p, L.sl_nxt, min(kTile, ntok - t0 - kTile));
-      L.load_idx(p, t_beg + t0 + 2 * kTile, last, L.sl_nxt);
-    }
-
-    // ---- scores for this wave's 16 tokens ------------------------------------
-    v4f s = v4f{0.f, 0.f, 0.f, 0.f};
-    const int trow = 16 * w + l16;
-    if constexpr (KF == 0) {
-      const uint8_t* kp = Klds + trow * C::KST;
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) s = mfma16_f8(ld_v8(kp + 128 * ks + 32 * g), qv[ks], s);
-      v8i a4 = g < 2 ? ld_v8(kp + 512 + 32 * g) : v8i{0, 0, 0, 0, 0, 0, 0, 0};
-      s = mfma16_f8(a4, qv[4], s);
-    } else {
-      const uint8_t* kp = Klds + trow * C::KST;
-      const uint8_t* sp = Slds + trow * 20;
-#pragma unroll
-      for (int ks = 0; ks < 5; ++ks) {
-        const int blk = 4 * ks + g;
-        v8i a = (blk < kMxBlocks) ? ld_v4_as_v8(kp + 16 * blk) : v8i{0, 0, 0, 0, 0, 0, 0, 0};
-        const int sc = (blk < kMxBlocks) ? (int)sp[blk] : 127;
-        s = mfma16_f4f8(a, sc, qv[ks], s);
+      lds_barrier();  // (2) P, its scales, the votes [and V^T] visible
+      if (__builtin_amdgcn_readfirstlane(*reinterpret_cast<const int*>(vote)) != 0) {
+        restart = true;
+        break;
       }
-    }
-    // s[r] = score(token 16w + 4g + r, head l16)
-    float sv[4];
-    float mx = neg_inf();
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int tok = 16 * w + 4 * g + r;
-      sv[r] = tok < nval ? s[r] * c : neg_inf();
-      mx = fmaxf(mx, sv[r]);
-    }
-    mx = fmaxf(mx, shfl_xor_f(mx, 16));
-    mx = fmaxf(mx, shfl_xor_f(mx, 32));
-    if (g == 0) wmax[w * 16 + l16] = mx;
-    __syncthreads();  // (B)
-    const float tmax = fmaxf(fmaxf(wmax[l16], wmax[16 + l16]), fmaxf(wmax[32 + l16], wmax[48 + l16]));
-    const float m_new = fmaxf(m_run, tmax);
-    const float alpha = exp2f(m_run - m_new);
-    m_run = m_new;
-    float pv[4];
-    float psum = 0.f;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      pv[r] = exp2f(sv[r] - m_new);
-      psum += pv[r];
-    }
-    l_run = l_run * alpha + psum;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) o[i] *= alpha;
-    if constexpr (!C::VB16) {
-      uint32_t hi, lo;
-      pack4_fp8_split(pv[0] * kPScale, pv[1] * kPScale, pv[2] * kPScale, pv[3] * kPScale, hi, lo);
-      *reinterpret_cast<uint32_t*>(Pl + l16 * C::PST + 16 * w + 4 * g) = hi;
-      *reinterpret_cast<uint32_t*>(Pl + 16 * C::PST + l16 * C::PST + 16 * w + 4 * g) = lo;
-    } else {
-      const uint32_t lo = f32_to_bf16_bits(pv[0]) | (f32_to_bf16_bits(pv[1]) << 16);
-      const uint32_t hi = f32_to_bf16_bits(pv[2]) | (f32_to_bf16_bits(pv[3]) << 16);
-      *reinterpret_cast<uint2*>(Pl + l16 * C::PST + 2 * (16 * w + 4 * g)) = make_uint2(lo, hi);
-    }
-    __syncthreads();  // (C) P visible
 
-    // ---- O^T[dims of this wave] += V^T . P^T --------------------------------
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
+      // ---- O^T[dims 128w ..] += V^T . P^T ---------------------------------------
       if constexpr (!C::VB16) {
-        const long bh = *reinterpret_cast<const long*>(Pl + l16 * C::PST + 32 * j + 8 * g);
-        const long bl = *reinterpret_cast<const long*>(Pl + 16 * C::PST + l16 * C::PST + 32 * j + 8 * g);
+        // The block-scaled MFMA takes fp8 byte j of lane group G as K index
+        // 16G + (j & 15) + 64 (j >> 4), scaled by lane group K/32.  Wave gw's
+        // 16 tokens therefore sit in K block gw: bytes 0-7 of group G hold
+        // tokens 8(G & 1) .. +7 of wave G/2, bytes 16-23 those of wave G/2 + 2,
+        // the other bytes are zero; lane group G supplies wave G's scale.
+        const int g0 = g >> 1, g1 = (g >> 1) + 2, ih = 8 * (g & 1);
+        const uint8_t* pb = smem + C::OFF_P + l16 * 16 + ih;
+        const uint2 h0 = *reinterpret_cast<const uint2*>(pb + g0 * 256);
+        const uint2 h1 = *reinterpret_cast<const uint2*>(pb + g1 * 256);
+        const uint2 q0 = *reinterpret_cast<const uint2*>(pb + 1024 + g0 * 256);
+        const uint2 q1 = *reinterpret_cast<const uint2*>(pb + 1024 + g1 * 256);
+        const v8i ph = v8i{(int)h0.x, (int)h0.y, 0, 0, (int)h1.x, (int)h1.y, 0, 0};
+        const v8i pl = v8i{(int)q0.x, (int)q0.y, 0, 0, (int)q1.x, (int)q1.y, 0, 0};
+        const int bsc = smem[C::OFF_PS + 16 * g + l16];
+        // transpose reads: row 16 g0 + ih + m (bytes 0-7) and 16 g1 + ih + m
+        // (bytes 16-23), dims 128w + 16dt + 8(lane & 1)
+        const int vst = VF == 1 ? C::VST : C::KST;
+        const uint32_t vb = lds0 + st * C::STAGE + (VF == 1 ? C::KW * 1024 : 0) + 128 * w + 8 * (lane & 1);
+        const int m = l16 >> 1;
+        const uint32_t a0 = vb + (16 * g0 + ih + m) * vst, a1 = vb + (16 * g1 + ih + m) * vst;
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt) {
-          const int d = 128 * w + 16 * dt + l16;
-          const long av = *reinterpret_cast<const long*>(Vt + vt16_read_off(d, 4 * j + g));
-          o[dt] = mfma16x32_f8(av, bh, o[dt]);
-          o[dt] = mfma16x32_f8(av, bl, o[dt]);
+          const v2i r0 = lds_read_tr8(a0 + 16 * dt);
+          const v2i r1 = lds_read_tr8(a1 + 16 * dt);
+          const v8i av = v8i{r0[0], r0[1], 0, 0, r1[0], r1[1], 0, 0};
+          o[dt] = mfma16_f8_bscale(av, ph, bsc, o[dt]);
+          o[dt] = mfma16_f8_bscale(av, pl, bsc, o[dt]);
         }
       } else {
-        const v8bf bq = *reinterpret_cast<const v8bf*>(Pl + l16 * C::PST + 2 * (32 * j + 8 * g));
+        const uint8_t* vt = smem + C::OFF_VT;
+        const uint8_t* pt = smem + C::OFF_P + l16 * C::VTST;
 #pragma unroll
-        for (int dt = 0; dt < 8; ++dt) {
-          const int d = 128 * w + 16 * dt + l16;
-          const v8bf av = *reinterpret_cast<const v8bf*>(Vt + d * C::VTST + 2 * (32 * j + 8 * g));
-          o[dt] = mfma16x32_bf16(av, bq, o[dt]);
+        for (int j = 0; j < 2; ++j) {
+          const v8bf bq = *reinterpret_cast<const v8bf*>(pt + 2 * (32 * j + 8 * g));
+#pragma unroll
+          for (int dt = 0; dt < 8; ++dt) {
+            const v8bf av = *reinterpret_cast<const v8bf*>(vt + (128 * w + 16 * dt + l16) * C::VTST + 2 * (32 * j + 8 * g));
+            o[dt] = mfma16x32_bf16(av, bq, o[dt]);
+          }
         }
       }
     }
-    __syncthreads();  // (D) LDS free for the next tile
-  };
-  for (int ti = 0; ti + 1 < ntiles; ++ti) tile(std::true_type{}, ti);
-  if (ntiles > 0) tile(std::false_type{}, ntiles - 1);
+    if (!restart) break;
+    // drain the ring (the prologue reuses it); m_ref = running max over the waves
+    wait_vmcnt<0>();
+    if (g == 0) xch[16 * w + l16] = m_seen;
+    lds_barrier();
+    m_ref = fmaxf(fmaxf(xch[l16], xch[16 + l16]), fmaxf(xch[32 + l16], xch[48 + l16]));
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = v4f{0.f, 0.f, 0.f, 0.f};
+    l_part = 0.f;
+    lds_barrier();  // exchange read before any rewrite
+  }
 
   // ---- finish: row sums across lanes and waves --------------------------------
-  float l = l_run;
+  float l = l_part;
   l += shfl_xor_f(l, 16);
   l += shfl_xor_f(l, 32);
-  if (g == 0) lsum[w * 16 + l16] = l;
-  __syncthreads();
-  const float Lsum = lsum[l16] + lsum[16 + l16] + lsum[32 + l16] + lsum[48 + l16];
-  const float inv = Lsum > 0.f ? vscale / Lsum : 0.f;
+  if (g == 0) xch[16 * w + l16] = l;
+  lds_barrier();
+  const float L = xch[l16] + xch[16 + l16] + xch[32 + l16] + xch[48 + l16];
+  const float inv = L > 0.f ? vscale / L : 0.f;
   const int head = l16;
   if (slot < 0) {
     uint16_t* orow = p.out + ((int64_t)b * 16 + head) * kVDim;
@@ -467,7 +478,7 @@ __global__ __launch_bounds__(256, 1) void decode_h16_kernel(const DecodeParams p
       *reinterpret_cast<float4*>(prow + d) =
           make_float4(o[dt][0] * inv, o[dt][1] * inv, o[dt][2] * inv, o[dt][3] * inv);
     }
-    if (w == 0 && g == 0) p.part_lse[(int64_t)slot * 16 + head] = Lsum > 0.f ? m_run + __log2f(Lsum) : neg_inf();
+    if (w == 0 && g == 0) p.part_lse[(int64_t)slot * 16 + head] = L > 0.f ? m_ref + __log2f(L) : neg_inf();
   }
 }
 

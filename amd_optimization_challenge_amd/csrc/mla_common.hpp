@@ -99,6 +99,10 @@ __device__ __forceinline__ float shfl_xor_f(float v, int mask) {
 __device__ __forceinline__ v4f mfma16_f8(v8i a, v8i b, v4f c) {
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
 }
+// fp8 x fp8 with an e8m0 scale on B (one per lane: its column, 32 K values)
+__device__ __forceinline__ v4f mfma16_f8_bscale(v8i a, v8i b, int b_scale, v4f c) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 127, 0, b_scale);
+}
 // Same shape, A = e2m1 (first four dwords) with an e8m0 scale per lane
 // (one per 32 K values), B = fp8 with unit scale.
 __device__ __forceinline__ v4f mfma16_f4f8(v8i a, int a_scale, v8i b, v4f c) {
@@ -149,6 +153,14 @@ __device__ __forceinline__ void dma16_to_lds(const void* g, uint32_t lds_off) {
 __device__ __forceinline__ void dma4_to_lds(const void* g, uint32_t lds_off) {
   uint32_t tmp;
   asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tglobal_load_lds_dword %2, off\n\ts_mov_b32 m0, %0"
+               : "=&s"(tmp)
+               : "s"(lds_off), "v"(g)
+               : "memory");
+}
+// one byte per lane: lane l's byte lands, zero-extended, in the dword at M0 + 4 l
+__device__ __forceinline__ void dma1_to_lds(const void* g, uint32_t lds_off) {
+  uint32_t tmp;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tglobal_load_lds_ubyte %2, off\n\ts_mov_b32 m0, %0"
                : "=&s"(tmp)
                : "s"(lds_off), "v"(g)
                : "memory");

@@ -76,6 +76,18 @@ __global__ void selftest_kernel(int which, const uint8_t* __restrict__ in, uint8
     v16f c = v16f{};
     c = which == 1 ? mfma32_f8(a, b, c) : mfma32_f4f8(a, sc, b, c);
     for (int r = 0; r < 16; ++r) D[(8 * (r / 4) + 4 * (l / 32) + (r % 4)) * 32 + (l % 32)] = c[r];
+  } else if (which == 15 || which == 16) {  // 16x16x128 fp8 with e8m0 scales on B (15) or A (16)
+    const uint8_t* A = in;
+    const uint8_t* B = in + 2048;
+    const uint8_t* Sc = in + 4096;  // [4 K blocks][16 cols (15) / rows (16)]
+    v8i a, b;
+    for (int i = 0; i < 8; ++i) a[i] = *reinterpret_cast<const int*>(A + (l % 16) * 128 + 32 * (l / 16) + 4 * i);
+    for (int i = 0; i < 8; ++i) b[i] = (int)gather4(B, 16, 32 * (l / 16) + 4 * i, l % 16);
+    const int sc = Sc[(l / 16) * 16 + (l % 16)];
+    v4f c = v4f{0.f, 0.f, 0.f, 0.f};
+    if (which == 15) c = mfma16_f8_bscale(a, b, sc, c);
+    else c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, sc, 0, 127);
+    for (int r = 0; r < 4; ++r) D[(4 * (l / 16) + r) * 16 + (l % 16)] = c[r];
   } else if (which == 4) {  // 16x16x32 fp8: A [16][32], B [32][16]
     const uint8_t* A = in;
     const uint8_t* B = in + 512;
@@ -161,6 +173,12 @@ __global__ void fp4_probe_kernel(int big, float* __restrict__ out) {
   }
 }
 
+// sub-dword LDS-DMA (probe 17; dma1_to_lds is the product's ubyte form)
+__device__ __forceinline__ void dma2_to_lds(const void* g, uint32_t lds_off) {
+  uint32_t tmp;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tglobal_load_lds_ushort %2, off\n\ts_mov_b32 m0, %0"
+               : "=&s"(tmp) : "s"(lds_off), "v"(g) : "memory");
+}
 // LDS-DMA placement (13) and ds_read_b64_tr_b8 (14).  in: 1024 source bytes.
 // 13: lane l DMAs src[16*((7l) % 64) ..+16] to LDS offsets 0, 65536+1024 and
 //     131072+4096; out = the three 1 KiB LDS windows.
@@ -177,6 +195,16 @@ __global__ void lds_probe_kernel(int which, const uint8_t* __restrict__ src, uin
     __syncthreads();
     for (int k = 0; k < 3; ++k)
       for (int i = 0; i < 16; ++i) out[k * 1024 + l * 16 + i] = lds[offs[k] + l * 16 + i];
+  } else if (which == 17 || which == 18) {
+    // 17: lane l DMAs the 2 bytes at src + 2l, 18: the byte at src + l, to M0 = 0;
+    // out = LDS bytes 0 .. 511 (pre-filled with 0xEE)
+    for (int i = l; i < 512; i += 64) lds[i] = 0xEE;
+    __syncthreads();
+    if (which == 17) dma2_to_lds(src + 2 * l, base);
+    else dma1_to_lds(src + l, base);
+    wait_vmcnt<0>();
+    __syncthreads();
+    for (int i = l; i < 512; i += 64) out[i] = lds[i];
   } else {
     for (int i = l; i < 4096; i += 64) lds[i] = src[i % 1024];
     __syncthreads();
@@ -188,7 +216,7 @@ __global__ void lds_probe_kernel(int which, const uint8_t* __restrict__ src, uin
 }
 
 hipError_t launch_selftest(int which, const void* in, void* out, hipStream_t stream) {
-  if (which == 13 || which == 14) {
+  if (which == 13 || which == 14 || which == 17 || which == 18) {
     hipLaunchKernelGGL(lds_probe_kernel, dim3(1), dim3(64), 0, stream, which,
                        static_cast<const uint8_t*>(in), static_cast<uint8_t*>(out));
     return hipGetLastError();
@@ -198,7 +226,7 @@ hipError_t launch_selftest(int which, const void* in, void* out, hipStream_t str
                        static_cast<float*>(out));
     return hipGetLastError();
   }
-  if (which < 0 || which > 10) return hipErrorInvalidValue;
+  if (which < 0 || (which > 10 && which != 15 && which != 16)) return hipErrorInvalidValue;
   hipLaunchKernelGGL(selftest_kernel, dim3(1), dim3(64), 0, stream, which,
                      static_cast<const uint8_t*>(in), static_cast<uint8_t*>(out));
   return hipGetLastError();

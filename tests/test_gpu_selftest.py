@@ -11,7 +11,7 @@ pytestmark = pytest.mark.gpu
 
 
 IN_BYTES = {0: 4096, 1: 4096, 2: 3136, 3: 3136, 4: 1024, 5: 2048, 6: 1024, 7: 512, 8: 1024, 9: 1024,
-            10: 256, 11: 0, 12: 0, 13: 1024, 14: 1024}
+            10: 256, 11: 0, 12: 0, 13: 1024, 14: 1024, 15: 4160, 16: 4160, 17: 1024, 18: 1024}
 
 
 def run(which, inp: np.ndarray, out_bytes: int) -> np.ndarray:
@@ -72,6 +72,36 @@ def test_mfma_scaled_fp4_by_fp8_layouts(cuda, which, M, N, K):
         errs[name] = float(np.max(np.abs(D - ref) / scale))
     print("fp4 hypotheses (max err / scale):", errs, flush=True)
     assert errs["low-nibble-first, scaled"] <= 1e-4, errs
+
+
+# Block-scaled 16x16x128 MFMA with fp8 operands: byte j of lane group G is K
+# index 16G + (j & 15) + 64 (j >> 4), and lane group b's scale covers K block
+# b = K // 32; so byte j of group G is scaled by group G // 2 + 2 (j >> 4).
+def scale_group_of_operand_row(k):
+    G, j = k // 32, k % 32
+    return G // 2 + 2 * (j >> 4)
+
+
+@pytest.mark.parametrize("which", [15, 16])
+def test_mfma_block_scales(cuda, which):
+    """16x16x128 fp8 with one e8m0 scale per lane (B: 15, A: 16); operands
+    loaded in the plain order (lane group G, byte j = row/col 32G + j)."""
+    rng = np.random.default_rng(20 + which)
+    A = fp8_codes(rng, (16, 128))
+    B = fp8_codes(rng, (128, 16))
+    Sc = rng.integers(120, 135, (4, 16)).astype(np.uint8)
+    D = run(which, np.concatenate([A.reshape(-1), B.reshape(-1), Sc.reshape(-1)]), 16 * 16 * 4)
+    D = D.view(np.float32).reshape(16, 16)
+    Af, Bf = O.e4m3fn_to_f32(A).astype(np.float64), O.e4m3fn_to_f32(B).astype(np.float64)
+    grp = np.array([scale_group_of_operand_row(k) for k in range(128)])
+    f = np.exp2(Sc.astype(np.float64) - 127)[grp]  # [k][col (15) or row (16)]
+    if which == 15:
+        Bf = Bf * f
+    else:
+        Af = Af * f.T
+    ref = Af @ Bf
+    scale = np.abs(Af) @ np.abs(Bf)
+    assert np.all(np.abs(D - ref) <= 1e-4 * scale), np.max(np.abs(D - ref) / scale)
 
 
 def test_mfma_bf16_layout(cuda):
@@ -179,3 +209,15 @@ def test_lds_transpose_read_b8(cuda):
             for m in range(8):
                 exp[l, m] = rows[16 * g + 2 * m + (j >> 3), j & 7]
         assert np.array_equal(got[pat], exp), pat
+
+
+@pytest.mark.parametrize("which,width", [(17, 2), (18, 1)])
+def test_lds_dma_subdword_placement(cuda, which, width):
+    """global_load_lds_ushort / _ubyte: lane l's bytes land zero-extended in
+    the dword at M0 + 4 l (the fp4 scale ring relies on the ubyte form)."""
+    src = (np.arange(1024) % 251 + 1).astype(np.uint8)
+    got = run(which, src, 512)
+    exp = np.zeros((64, 4), np.uint8)
+    exp[:, :width] = src[: 64 * width].reshape(64, width)
+    assert np.array_equal(got[:256].reshape(64, 4), exp)
+    assert np.all(got[256:] == 0xEE)
