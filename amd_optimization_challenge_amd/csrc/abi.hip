@@ -71,7 +71,9 @@ int check_shape(int batch, int num_heads, int kv_mode) {
 // kernels fit two per CU, the others one), raised to 2 per sequence when the
 // batch is large so long sequences still get split, capped at 4 rounds.
 int target_items_for(int batch, int num_heads, int kv_mode, int num_cu) {
-  const int slots = (num_heads == 16 && kv_mode != MLA_KV_MXFP4) ? 2 * num_cu : num_cu;
+  (void)num_heads;
+  (void)kv_mode;
+  const int slots = num_cu;  // one resident work-group per CU (the LDS ring fills the CU)
   int t = 2 * batch > slots ? 2 * batch : slots;
   return t < 4 * slots ? t : 4 * slots;
 }
@@ -152,6 +154,9 @@ int decode_params(const void* q_fp8, const float* q_scale, const void* k_cache, 
   p->part_o = reinterpret_cast<float*>(ws + L->part_o_off);
   p->part_lse = reinterpret_cast<float*>(ws + L->part_lse_off);
   p->out = static_cast<uint16_t*>(out);
+  p->q_bf16 = nullptr;
+  p->q_partials = nullptr;
+  p->q_nparts = 0;
   p->sm_scale = sm_scale;
   p->batch = batch;
   p->num_heads = num_heads;
@@ -197,8 +202,8 @@ int mla_quant_fp8_per_tensor(const void* x_bf16, int64_t n, void* out_fp8, float
   hipStream_t s = static_cast<hipStream_t>(stream);
   uint32_t* partials = static_cast<uint32_t*>(workspace);
   int nb = 0;
-  hipError_t e = launch_amax(static_cast<const uint16_t*>(x_bf16), n, partials, &nb, nullptr, 0, 0, 0,
-                             nullptr, s);
+  hipError_t e = launch_amax(static_cast<const uint16_t*>(x_bf16), n, partials, &nb, nullptr, nullptr, 0, 0,
+                             0, nullptr, s);
   if (e != hipSuccess) return hip_fail(e, "amax launch");
   e = launch_quant_fp8(static_cast<const uint16_t*>(x_bf16), n, partials, nb,
                        static_cast<uint8_t*>(out_fp8), out_scale, s);
@@ -314,12 +319,19 @@ int mla_decode_fwd(const void* q_bf16, const void* k_cache, int64_t k_row_stride
   const int64_t n = (int64_t)batch * num_heads * kQKDim;
   uint32_t* partials = reinterpret_cast<uint32_t*>(ws + L.quant_off);
   int nb = 0;
-  hipError_t e = launch_amax(static_cast<const uint16_t*>(q_bf16), n, partials, &nb, kv_indptr, batch,
-                             L.target_items, L.max_items,
+  hipError_t e = launch_amax(static_cast<const uint16_t*>(q_bf16), n, partials, &nb, kv_indptr,
+                             static_cast<const int32_t*>(kv_indices), batch, L.target_items, L.max_items,
                              reinterpret_cast<int32_t*>(ws + L.plan_off), s);
   if (e != hipSuccess) return hip_fail(e, "amax+plan launch");
-  e = launch_quant_fp8(static_cast<const uint16_t*>(q_bf16), n, partials, nb, q_fp8, q_scale, s);
-  if (e != hipSuccess) return hip_fail(e, "quant launch");
+  if (num_heads == 16) {
+    // the H = 16 kernel quantizes its sequence's Q from the amax partials
+    p.q_bf16 = static_cast<const uint16_t*>(q_bf16);
+    p.q_partials = partials;
+    p.q_nparts = nb;
+  } else {
+    e = launch_quant_fp8(static_cast<const uint16_t*>(q_bf16), n, partials, nb, q_fp8, q_scale, s);
+    if (e != hipSuccess) return hip_fail(e, "quant launch");
+  }
   e = launch_decode(p, kv_mode, L.max_items, s);
   if (e != hipSuccess) return hip_fail(e, "decode launch");
   e = launch_combine(p, s);

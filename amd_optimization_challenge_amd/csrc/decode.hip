@@ -136,7 +136,7 @@ struct H16 {
   static constexpr int LDS = OFF_VOTE + 16;
 };
 
-template <int KF, int VF, bool IDX>
+template <int KF, int VF, bool IDX, bool QB>
 __global__ __launch_bounds__(256, 1) void decode_h16_kernel(const DecodeParams p) {
   using C = H16<KF, VF>;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[C::LDS];
@@ -161,25 +161,66 @@ __global__ __launch_bounds__(256, 1) void decode_h16_kernel(const DecodeParams p
   // g' where 32g + e = 16g' + (i & 15) + 64 (i >> 4); the fp8 Q operand is
   // gathered in that order.  With fp8 K both operands share one order.
   v8i qv[5];
+  float qs;
   {
-    const uint8_t* qrow = p.q_fp8 + ((int64_t)b * 16 + l16) * kQKDim;
-    if constexpr (KF == 0) {
+    auto load_q = [&](const uint8_t* qrow) {
+      if constexpr (KF == 0) {
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) qv[ks] = ld_v8(qrow + 128 * ks + 32 * g);
-      qv[4] = g < 2 ? ld_v8(qrow + 512 + 32 * g) : v8i{0, 0, 0, 0, 0, 0, 0, 0};
-    } else {
+        for (int ks = 0; ks < 4; ++ks) qv[ks] = ld_v8(qrow + 128 * ks + 32 * g);
+        qv[4] = g < 2 ? ld_v8(qrow + 512 + 32 * g) : v8i{0, 0, 0, 0, 0, 0, 0, 0};
+      } else {
 #pragma unroll
-      for (int ks = 0; ks < 5; ++ks) {
-        const uint4 lo = *reinterpret_cast<const uint4*>(qrow + 128 * ks + 16 * g);
-        const uint4 hi = ks < 4 ? *reinterpret_cast<const uint4*>(qrow + 128 * ks + 64 + 16 * g)
-                                : make_uint4(0, 0, 0, 0);
-        qv[ks] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+        for (int ks = 0; ks < 5; ++ks) {
+          const uint4 lo = *reinterpret_cast<const uint4*>(qrow + 128 * ks + 16 * g);
+          const uint4 hi = ks < 4 ? *reinterpret_cast<const uint4*>(qrow + 128 * ks + 64 + 16 * g)
+                                  : make_uint4(0, 0, 0, 0);
+          qv[ks] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+        }
       }
+    };
+    if constexpr (QB) {
+      // Q quantized here (bit-exact with the quant kernel): the per-tensor
+      // scale is folded from the amax partials, and this sequence's 16 x 576
+      // fp8 Q is staged row-major in the last ring stage (its first DMA comes
+      // after the first tile barrier)
+      uint8_t* qst = smem + (C::S - 1) * C::STAGE;
+      const uint4* src = reinterpret_cast<const uint4*>(p.q_bf16 + (int64_t)b * 16 * kQKDim);
+      constexpr int NV = 16 * kQKDim / 8, NJ = (NV + 255) / 256;
+      uint4 xv[NJ];
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const int i = tid + 256 * j;
+        if (i < NV) xv[j] = src[i];
+      }
+      uint32_t m = 0;
+      for (int i = tid; i < p.q_nparts; i += 256) m = max(m, p.q_partials[i]);
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, off, 64));
+      uint32_t* xu = reinterpret_cast<uint32_t*>(smem + C::OFF_X);
+      if (lane == 0) xu[w] = m;
+      lds_barrier();
+      qs = fp8_scale_from_amax(max(max(xu[0], xu[1]), max(xu[2], xu[3])));
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const int i = tid + 256 * j;
+        if (i < NV) {
+          const uint32_t wv[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
+          uint32_t o2[2] = {0, 0};
+#pragma unroll
+          for (int k = 0; k < 4; ++k)
+            o2[k >> 1] |= (quant_one(wv[k] & 0xFFFFu, qs) | (quant_one(wv[k] >> 16, qs) << 8)) << (16 * (k & 1));
+          *reinterpret_cast<uint2*>(qst + 8 * i) = make_uint2(o2[0], o2[1]);
+        }
+      }
+      lds_barrier();
+      load_q(qst + l16 * kQKDim);
+    } else {
+      qs = p.q_scale[0];
+      load_q(p.q_fp8 + ((int64_t)b * 16 + l16) * kQKDim);
     }
 #pragma unroll
     for (int ks = 0; ks < 5; ++ks) asm volatile("" : "+v"(qv[ks]));  // keep resident, no reload
   }
-  const float qs = p.q_scale[0];
   const float kvs = (KF == 0 || VF == 1) ? p.kv_scale[0] : 1.0f;
   const float c = qs * (KF == 0 ? kvs : 1.0f) * p.sm_scale * kLog2e;
   const float vscale = VF == 2 ? 1.0f : kvs;
@@ -208,22 +249,28 @@ __global__ __launch_bounds__(256, 1) void decode_h16_kernel(const DecodeParams p
     if (w < C::RW0) return;
     const int st = t % C::S;
     const uint32_t sbase = lds0 + st * C::STAGE;
+    // all slot reads first: each DMA below is an asm barrier for memory ops
+    int sl[C::NA], co[C::NA];
 #pragma unroll
     for (int k = 0; k < C::NA; ++k) {
       const int u = (w - C::RW0) + C::NRW * k;
-      if (u < C::NW) {
-        const uint8_t* src;
-        if (u < C::KW) {
-          const int e = 64 * u + lane;  // 16-B chunk index within the stage
-          const int tok = e / C::KCPR, ch = e - tok * C::KCPR;
-          src = p.k_cache + (int64_t)slot_of(t, tok) * p.k_row_stride + 16 * min(ch, C::KCH - 1);
-        } else {
-          const int e = 64 * (u - C::KW) + lane;
-          const int tok = e / C::VCPR, ch = e - tok * C::VCPR;
-          src = p.v_cache + (int64_t)slot_of(t, tok) * p.v_row_stride + 16 * min(ch, 31);
-        }
-        dma16_to_lds(src, sbase + 1024 * u);
+      if (u < C::KW) {
+        const int e = 64 * u + lane;  // 16-B chunk index within the stage
+        const int tok = e / C::KCPR, ch = e - tok * C::KCPR;
+        sl[k] = slot_of(t, tok);
+        co[k] = 16 * min(ch, C::KCH - 1);
+      } else if (u < C::NW) {
+        const int e = 64 * (u - C::KW) + lane;
+        const int tok = e / C::VCPR, ch = e - tok * C::VCPR;
+        sl[k] = slot_of(t, tok);
+        co[k] = 16 * min(ch, 31);
       }
+    }
+#pragma unroll
+    for (int k = 0; k < C::NA; ++k) {
+      const int u = (w - C::RW0) + C::NRW * k;
+      if (u < C::KW) dma16_to_lds(p.k_cache + (int64_t)sl[k] * p.k_row_stride + co[k], sbase + 1024 * u);
+      else if (u < C::NW) dma16_to_lds(p.v_cache + (int64_t)sl[k] * p.v_row_stride + co[k], sbase + 1024 * u);
     }
   };
   // fp4 K scales: wave 0 DMAs the 18 e8m0 bytes of token `lane` of tile t, one
@@ -292,21 +339,26 @@ __global__ __launch_bounds__(256, 1) void decode_h16_kernel(const DecodeParams p
       // ---- scores: rows i = l16 of this wave's slice, 16x16x128 MFMAs ----------
       v4f s = v4f{0.f, 0.f, 0.f, 0.f};
       {
+        // all fragment reads first, then the MFMA chain
         const uint8_t* kp = kt + tok_of(w, l16) * C::KST;
+        v8i ka[5];
         if constexpr (KF == 0) {
 #pragma unroll
-          for (int ks = 0; ks < 4; ++ks) s = mfma16_f8(ld_v8(kp + 128 * ks + 32 * g), qv[ks], s);
-          const v8i a4 = g < 2 ? ld_v8(kp + 512 + 32 * g) : v8i{0, 0, 0, 0, 0, 0, 0, 0};
-          s = mfma16_f8(a4, qv[4], s);
+          for (int ks = 0; ks < 4; ++ks) ka[ks] = ld_v8(kp + 128 * ks + 32 * g);
+          ka[4] = g < 2 ? ld_v8(kp + 512 + 32 * g) : v8i{0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+          for (int ks = 0; ks < 5; ++ks) s = mfma16_f8(ka[ks], qv[ks], s);
         } else {
           const uint8_t* sp = sct + 4 * tok_of(w, l16);
+          int ksc[5];
 #pragma unroll
           for (int ks = 0; ks < 5; ++ks) {
             const int blk = 4 * ks + g;
-            const v8i a = blk < kMxBlocks ? ld_v4_as_v8(kp + 16 * blk) : v8i{0, 0, 0, 0, 0, 0, 0, 0};
-            const int sc = blk < kMxBlocks ? (int)sp[256 * blk] : 127;
-            s = mfma16_f4f8(a, sc, qv[ks], s);
+            ka[ks] = blk < kMxBlocks ? ld_v4_as_v8(kp + 16 * blk) : v8i{0, 0, 0, 0, 0, 0, 0, 0};
+            ksc[ks] = blk < kMxBlocks ? (int)sp[256 * blk] : 127;
           }
+#pragma unroll
+          for (int ks = 0; ks < 5; ++ks) s = mfma16_f4f8(ka[ks], ksc[ks], qv[ks], s);
         }
       }
       // s[r] = score(token tok_of(w, 4g + r), head l16)
@@ -418,25 +470,29 @@ __global__ __launch_bounds__(256, 1) void decode_h16_kernel(const DecodeParams p
         const uint32_t vb = lds0 + st * C::STAGE + (VF == 1 ? C::KW * 1024 : 0) + 128 * w + 8 * (lane & 1);
         const int m = l16 >> 1;
         const uint32_t a0 = vb + (16 * g0 + ih + m) * vst, a1 = vb + (16 * g1 + ih + m) * vst;
+        v2i r0[8], r1[8];
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt) {
-          const v2i r0 = lds_read_tr8(a0 + 16 * dt);
-          const v2i r1 = lds_read_tr8(a1 + 16 * dt);
-          const v8i av = v8i{r0[0], r0[1], 0, 0, r1[0], r1[1], 0, 0};
+          r0[dt] = lds_read_tr8(a0 + 16 * dt);
+          r1[dt] = lds_read_tr8(a1 + 16 * dt);
+        }
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+          const v8i av = v8i{r0[dt][0], r0[dt][1], 0, 0, r1[dt][0], r1[dt][1], 0, 0};
           o[dt] = mfma16_f8_bscale(av, ph, bsc, o[dt]);
           o[dt] = mfma16_f8_bscale(av, pl, bsc, o[dt]);
         }
       } else {
-        const uint8_t* vt = smem + C::OFF_VT;
-        const uint8_t* pt = smem + C::OFF_P + l16 * C::VTST;
+        const uint8_t* vt = smem + C::OFF_VT + (128 * w + l16) * C::VTST + 16 * g;
+        const uint8_t* pt = smem + C::OFF_P + l16 * C::VTST + 16 * g;
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-          const v8bf bq = *reinterpret_cast<const v8bf*>(pt + 2 * (32 * j + 8 * g));
+          const v8bf bq = *reinterpret_cast<const v8bf*>(pt + 64 * j);
+          v8bf av[8];
 #pragma unroll
-          for (int dt = 0; dt < 8; ++dt) {
-            const v8bf av = *reinterpret_cast<const v8bf*>(vt + (128 * w + 16 * dt + l16) * C::VTST + 2 * (32 * j + 8 * g));
-            o[dt] = mfma16x32_bf16(av, bq, o[dt]);
-          }
+          for (int dt = 0; dt < 8; ++dt) av[dt] = *reinterpret_cast<const v8bf*>(vt + 16 * dt * C::VTST + 64 * j);
+#pragma unroll
+          for (int dt = 0; dt < 8; ++dt) o[dt] = mfma16x32_bf16(av[dt], bq, o[dt]);
         }
       }
     }
@@ -817,59 +873,70 @@ __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams 
 
 // ============================================================================
 // LSE combine: out[b,h,:] = sum_s 2^(lse_s - M) O_s / sum_s 2^(lse_s - M)
-// grid (batch, H/16), 256 threads: thread = (head in group, 32-dim slice)
+// grid (batch, H/16, 4): block = 16 heads x 128 dims, thread = (head, 8 dims);
+// the split partials are read in batches of 8 so their loads overlap
 // ============================================================================
 __global__ __launch_bounds__(256) void combine_kernel(const DecodeParams p) {
-  const int b = blockIdx.x;
-  const int H = p.num_heads;
-  const int2* binfo = reinterpret_cast<const int2*>(p.plan + kPlanHeader + 4 * p.max_items);
-  const int2 bi = binfo[b];
+  const int b = blockIdx.x, H = p.num_heads;
+  const int2 bi = reinterpret_cast<const int2*>(p.plan + kPlanHeader + 4 * p.max_items)[b];
   if (bi.y <= 1) return;
   const int head = blockIdx.y * 16 + (threadIdx.x >> 4);
-  const int d0 = (threadIdx.x & 15) * 32;
+  const int d0 = blockIdx.z * 128 + (threadIdx.x & 15) * 8;
+  const float* lse = p.part_lse + (int64_t)bi.x * H + head;
   float M = neg_inf();
-  for (int s = 0; s < bi.y; ++s) M = fmaxf(M, p.part_lse[(int64_t)(bi.x + s) * H + head]);
-  float acc[32];
+  for (int s = 0; s < bi.y; ++s) M = fmaxf(M, lse[(int64_t)s * H]);
+  float acc[8];
 #pragma unroll
-  for (int i = 0; i < 32; ++i) acc[i] = 0.f;
+  for (int i = 0; i < 8; ++i) acc[i] = 0.f;
   float wsum = 0.f;
   if (M != neg_inf()) {
-    for (int s = 0; s < bi.y; ++s) {
-      const int64_t slot = bi.x + s;
-      const float wgt = exp2f(p.part_lse[slot * H + head] - M);
-      wsum += wgt;
-      const float4* src = reinterpret_cast<const float4*>(p.part_o + (slot * H + head) * kVDim + d0);
+    const float* po = p.part_o + ((int64_t)bi.x * H + head) * kVDim + d0;
+    const int64_t sstride = (int64_t)H * kVDim;
+    for (int s0 = 0; s0 < bi.y; s0 += 8) {
+      float4 v[8][2];
+      float wg[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        float4 v = src[i];
-        acc[4 * i + 0] += wgt * v.x;
-        acc[4 * i + 1] += wgt * v.y;
-        acc[4 * i + 2] += wgt * v.z;
-        acc[4 * i + 3] += wgt * v.w;
+      for (int j = 0; j < 8; ++j) {
+        const int s = min(s0 + j, bi.y - 1);
+        const float4* src = reinterpret_cast<const float4*>(po + s * sstride);
+        v[j][0] = src[0];
+        v[j][1] = src[1];
+        wg[j] = s0 + j < bi.y ? exp2f(lse[(int64_t)s * H] - M) : 0.f;
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        wsum += wg[j];
+        acc[0] += wg[j] * v[j][0].x;
+        acc[1] += wg[j] * v[j][0].y;
+        acc[2] += wg[j] * v[j][0].z;
+        acc[3] += wg[j] * v[j][0].w;
+        acc[4] += wg[j] * v[j][1].x;
+        acc[5] += wg[j] * v[j][1].y;
+        acc[6] += wg[j] * v[j][1].z;
+        acc[7] += wg[j] * v[j][1].w;
       }
     }
   }
   const float inv = wsum > 0.f ? 1.0f / wsum : 0.f;
-  uint16_t* orow = p.out + ((int64_t)b * H + head) * kVDim + d0;
+  uint32_t w4[4];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const uint32_t lo = f32_to_bf16_bits(acc[4 * i] * inv) | (f32_to_bf16_bits(acc[4 * i + 1] * inv) << 16);
-    const uint32_t hi = f32_to_bf16_bits(acc[4 * i + 2] * inv) | (f32_to_bf16_bits(acc[4 * i + 3] * inv) << 16);
-    *reinterpret_cast<uint2*>(orow + 4 * i) = make_uint2(lo, hi);
-  }
+  for (int i = 0; i < 4; ++i)
+    w4[i] = f32_to_bf16_bits(acc[2 * i] * inv) | (f32_to_bf16_bits(acc[2 * i + 1] * inv) << 16);
+  *reinterpret_cast<uint4*>(p.out + ((int64_t)b * H + head) * kVDim + d0) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
 }
 
 // ============================================================================
-template <bool IDX>
+template <bool IDX, bool QB>
 static hipError_t launch_decode_t(const DecodeParams& p, int kv_mode, int grid, hipStream_t stream) {
   if (p.num_heads == 16) {
     switch (kv_mode) {
-      case 0: hipLaunchKernelGGL((decode_h16_kernel<0, 0, IDX>), dim3(grid), dim3(256), 0, stream, p); break;
-      case 1: hipLaunchKernelGGL((decode_h16_kernel<1, 2, IDX>), dim3(grid), dim3(256), 0, stream, p); break;
-      case 2: hipLaunchKernelGGL((decode_h16_kernel<1, 1, IDX>), dim3(grid), dim3(256), 0, stream, p); break;
+      case 0: hipLaunchKernelGGL((decode_h16_kernel<0, 0, IDX, QB>), dim3(grid), dim3(256), 0, stream, p); break;
+      case 1: hipLaunchKernelGGL((decode_h16_kernel<1, 2, IDX, QB>), dim3(grid), dim3(256), 0, stream, p); break;
+      case 2: hipLaunchKernelGGL((decode_h16_kernel<1, 1, IDX, QB>), dim3(grid), dim3(256), 0, stream, p); break;
       default: return hipErrorInvalidValue;
     }
   } else if (p.num_heads == 128) {
+    if (QB) return hipErrorInvalidValue;  // the H = 128 kernel takes a quantized Q
     switch (kv_mode) {
       case 0: hipLaunchKernelGGL((decode_h128_kernel<0, IDX>), dim3(grid), dim3(256), 0, stream, p); break;
       case 2: hipLaunchKernelGGL((decode_h128_kernel<1, IDX>), dim3(grid), dim3(256), 0, stream, p); break;
@@ -882,12 +949,15 @@ static hipError_t launch_decode_t(const DecodeParams& p, int kv_mode, int grid, 
 }
 
 hipError_t launch_decode(const DecodeParams& p, int kv_mode, int grid, hipStream_t stream) {
-  return p.kv_indices != nullptr ? launch_decode_t<true>(p, kv_mode, grid, stream)
-                                 : launch_decode_t<false>(p, kv_mode, grid, stream);
+  const bool idx = p.kv_indices != nullptr, qb = p.q_bf16 != nullptr;
+  if (idx) return qb ? launch_decode_t<true, true>(p, kv_mode, grid, stream)
+                     : launch_decode_t<true, false>(p, kv_mode, grid, stream);
+  return qb ? launch_decode_t<false, true>(p, kv_mode, grid, stream)
+            : launch_decode_t<false, false>(p, kv_mode, grid, stream);
 }
 
 hipError_t launch_combine(const DecodeParams& p, hipStream_t stream) {
-  hipLaunchKernelGGL(combine_kernel, dim3(p.batch, p.num_heads / 16), dim3(256), 0, stream, p);
+  hipLaunchKernelGGL(combine_kernel, dim3(p.batch, p.num_heads / 16, 4), dim3(256), 0, stream, p);
   return hipGetLastError();
 }
 

@@ -37,6 +37,11 @@ struct DecodeParams {
   float* part_o;             // [max_items, H, 512]
   float* part_lse;           // [max_items, H]  (log2 domain)
   uint16_t* out;             // [B, H, 512] bf16
+  // Q as bf16 with the per-tensor amax partials (the H = 16 kernel quantizes
+  // its sequence's Q itself); q_fp8 / q_scale are used when q_bf16 is null
+  const uint16_t* q_bf16;    // [B, H, 576] or nullptr
+  const uint32_t* q_partials;
+  int q_nparts;
   float sm_scale;
   int batch;
   int num_heads;
@@ -86,6 +91,21 @@ __device__ __forceinline__ uint32_t f32_to_e4m3fn(float f) {
     code = (u >> 20) - (120u << 3);
   }
   return sign | code;
+}
+
+// bf16 |x|max bits -> f32 scale exactly as torch evaluates
+// competitor_submissions/mi355x_reference/reference.py:77-78
+__device__ __forceinline__ float fp8_scale_from_amax(uint32_t amax_bits) {
+  amax_bits = amax_bits > 0x2B8Du ? amax_bits : 0x2B8Du;  // clamp(min=1e-12) in bf16
+  const float a = bf16_bits_to_f32(amax_bits);
+  return bf16_bits_to_f32(f32_to_bf16_bits(a / 448.0f));
+}
+
+// y = e4m3fn(clamp(bf16(x / s), -448, 448)), reference.py:79-80
+__device__ __forceinline__ uint32_t quant_one(uint32_t h, float s) {
+  float y = bf16_bits_to_f32(f32_to_bf16_bits(bf16_bits_to_f32(h) / s));
+  y = fminf(fmaxf(y, -448.0f), 448.0f);
+  return f32_to_e4m3fn(y);
 }
 
 // ---- wave helpers ------------------------------------------------------------

@@ -223,7 +223,7 @@ def _a256(x: int) -> int:
 def workspace_layout(batch: int, num_heads: int, kv_mode, num_cu: int) -> dict:
     """Byte offsets of the workspace regions; ``total`` equals mla_workspace_bytes."""
     mode = kv_mode_id(kv_mode)
-    slots = 2 * num_cu if (num_heads == 16 and mode != 1) else num_cu
+    slots = num_cu  # one resident work-group per CU (the LDS ring fills the CU)
     target = min(max(slots, 2 * batch), 4 * slots)
     max_items = max(min(max(2 * num_cu, 2 * batch), 8 * num_cu), batch)
     off = 0
@@ -250,6 +250,6 @@ def read_plan(ws: torch.Tensor, batch: int, num_heads: int, kv_mode) -> dict:
     hdr = words[:PLAN_HEADER]
     n = int(hdr[0])
     items = words[PLAN_HEADER: PLAN_HEADER + 4 * mi].reshape(mi, 4)[:n]
-    binfo = words[PLAN_HEADER + 4 * mi:].reshape(batch, 2)
+    binfo = words[PLAN_HEADER + 4 * mi: PLAN_HEADER + 4 * mi + 2 * batch].reshape(batch, 2)
     return {"num_items": n, "chunk": int(hdr[1]), "total": int(hdr[2]), "batch": int(hdr[3]),
             "max_items": int(hdr[4]), "items": items, "batch_info": binfo, "layout": lay}

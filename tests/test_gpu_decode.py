@@ -105,3 +105,33 @@ def test_golden_decode_fixture(cuda):
     out = custom_kernel((q, kv_data, None, torch.from_numpy(d["kv_indptr"]).to(dev), cfg))
     assert_close(out.float().cpu().numpy(), d["out_f32"])
     assert O.f32_to_bf16(d["out_f32"]).shape == tuple(out.shape)
+
+
+@pytest.mark.parametrize("heads,mode", MODES)
+def test_fused_pipeline_matches_staged(cuda, heads, mode):
+    """custom_kernel (for H = 16 the decode kernel quantizes Q itself from
+    the amax partials) equals the staged entry points (quant kernel, plan,
+    decode, combine) bit for bit, and a second decode + combine on the same
+    plan reproduces it."""
+    from amd_optimization_challenge_amd import ops
+
+    print(f"fused vs staged H={heads} mode={mode}", flush=True)
+    q, kv, indptr, idx, qb, caches = host_case([3000, 10, 129, 700, 1], heads, mode, seed=41)
+    data = device_data(q, kv, indptr, idx, caches, mode, 0.07)
+    fused = custom_kernel(data)
+    qd, kv_data, _, kv_indptr, cfg = data
+    B = qd.shape[0]
+    ws = ops.workspace(B, heads, mode, qd.device)
+    qf8 = torch.empty(qd.shape, dtype=torch.float8_e4m3fn, device=qd.device)
+    qsc = torch.empty(1, dtype=torch.float32, device=qd.device)
+    ops.quant_fp8_per_tensor(qd, qf8, qsc)
+    ops.plan(kv_indptr, B, heads, mode, ws)
+    outs = []
+    for _ in range(2):
+        out = torch.full((B, heads, 512), float("nan"), dtype=torch.bfloat16, device=qd.device)
+        ops.decode(qf8, qsc, kv_data, kv_indptr, cfg["kv_indices"], heads, cfg["sm_scale"], mode, ws, out)
+        ops.combine(B, heads, ws, out)
+        outs.append(out)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], fused)
+    assert torch.equal(outs[1], fused)
