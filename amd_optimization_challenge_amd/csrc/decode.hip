@@ -627,23 +627,34 @@ __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams 
     const int st = t % C::S;
     const int pos0 = t_beg + kTile * t;
     const uint32_t sbase = lds0 + st * C::STAGE;
+    // all slot reads first: each DMA below is an asm barrier for memory ops
+    int sl[C::DPW], co[C::DPW];
 #pragma unroll
     for (int k = 0; k < C::DPW; ++k) {
       const int u = w + 4 * k;  // window index within the stage
-      const uint8_t* src;
       if (u < C::KDMA) {
         const int bb = 1024 * u + 16 * lane;
         int tok = bb / C::KST, pos = (bb - tok * C::KST) >> 4;
         if (tok >= kTile) { tok = kTile - 1; pos = 0; }
-        src = p.k_cache + (int64_t)slot_of(st, tok, pos0) * p.k_row_stride + 16 * min(pos, C::KCH - 1);
+        sl[k] = slot_of(st, tok, pos0);
+        co[k] = 16 * min(pos, C::KCH - 1);
       } else if (KF == 1 && u < C::KDMA + C::VDMA) {
         const int bb = 1024 * (u - C::KDMA) + 16 * lane;
         int tok = bb / C::VST, pos = (bb - tok * C::VST) >> 4;
         if (tok >= kTile) { tok = kTile - 1; pos = 0; }
-        src = p.v_cache + (int64_t)slot_of(st, tok, pos0) * p.v_row_stride + 16 * min(pos, 31);
+        sl[k] = slot_of(st, tok, pos0);
+        co[k] = 16 * min(pos, 31);
       } else {  // padding window: any valid source
-        src = p.k_cache + (int64_t)slot_of(st, kTile - 1, pos0) * p.k_row_stride;
+        sl[k] = slot_of(st, kTile - 1, pos0);
+        co[k] = 0;
       }
+    }
+#pragma unroll
+    for (int k = 0; k < C::DPW; ++k) {
+      const int u = w + 4 * k;
+      const bool vrow = KF == 1 && u >= C::KDMA && u < C::KDMA + C::VDMA;
+      const uint8_t* src = vrow ? p.v_cache + (int64_t)sl[k] * p.v_row_stride + co[k]
+                                : p.k_cache + (int64_t)sl[k] * p.k_row_stride + co[k];
       dma16_to_lds(src, sbase + 1024 * u);
     }
   };
@@ -701,7 +712,7 @@ __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams 
   // rescaled.  A tile whose max lies more than kRebase above m_ref (the
   // accumulators could overflow) makes the whole block restart the item with
   // m_ref = the running max: a block-wide vote through LDS, one tile late.
-  volatile uint8_t* vote = smem + C::OFF_VOTE;  // [2][4] wave flags, double-buffered by tile parity
+  uint8_t* vote = smem + C::OFF_VOTE;  // [2][4] wave flags, double-buffered by tile parity
   float m_seen = neg_inf();
   bool have_ref = false;
   for (;;) {
@@ -724,7 +735,7 @@ __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams 
         for (int ks = 0; ks < 9; ++ks) sc_cur[u][ks] = sc_nxt[u][ks];
     }
     lds_barrier();  // tile ti visible; the stage of tile ti-1 is free
-    if (ti > 0 && __builtin_amdgcn_readfirstlane(*reinterpret_cast<volatile uint32_t*>(vote + 4 * ((ti - 1) & 1))) != 0) {
+    if (ti > 0 && __builtin_amdgcn_readfirstlane(*reinterpret_cast<const uint32_t*>(vote + 4 * ((ti - 1) & 1))) != 0) {
       restart = true;
       break;
     }
@@ -762,45 +773,55 @@ __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams 
       __builtin_amdgcn_sched_barrier(0);
     }
     (void)sb;
-    // s_u[r] = score(token 32u + 8(r/4) + 4hh + r%4, head)
-    float mx = neg_inf();
+    // s_u[r] = raw score(token 32u + 8(r/4) + 4hh + r%4, head); masked on a partial tile
+    if (nval < kTile) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int tk = 8 * (r >> 2) + 4 * hh + (r & 3);
+        if (tk >= nval) s0[r] = neg_inf();
+        if (32 + tk >= nval) s1[r] = neg_inf();
+      }
+    }
+    float mx0 = neg_inf(), mx1 = neg_inf();
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int tk = 8 * (r >> 2) + 4 * hh + (r & 3);
-      s0[r] = tk < nval ? s0[r] * c : neg_inf();
-      s1[r] = 32 + tk < nval ? s1[r] * c : neg_inf();
-      mx = fmaxf(mx, fmaxf(s0[r], s1[r]));
+      mx0 = fmaxf(mx0, s0[r]);
+      mx1 = fmaxf(mx1, s1[r]);
     }
-    mx = fmaxf(mx, shfl_xor_f(mx, 32));
-    // Fixed per-item reference m_ref (the first tile's ceil(max)); each tile's
-    // offset rides on the B-operand e8m0 scale of the PV MFMA, so O^T is never
+    mx0 = fmaxf(mx0, shfl_xor_f(mx0, 32));
+    mx1 = fmaxf(mx1, shfl_xor_f(mx1, 32));
+    // Per-item reference m_ref (the first tile's ceil max) and per-half offsets
+    // m_u = ceil(c max_u) (c > 0: the quantization scales are positive).  Half u
+    // is K block u of the PV MFMA, whose e8m0 B scale comes from lane group u
+    // (hh = u), so each half carries 2^(m_u - m_ref - 8) and O^T is never
     // rescaled: O^T accumulates sum_n V_n 2^(s_n - m_ref).
-    const float m_t = __builtin_ceilf(mx);
-    if (!have_ref) m_ref = m_t;  // first tile of the first pass
+    const float m0 = __builtin_ceilf(mx0 * c), m1 = __builtin_ceilf(mx1 * c);  // -inf: empty half
+    const float mt = fmaxf(m0, m1);
+    if (!have_ref) m_ref = mt;  // first tile of the first pass
     have_ref = true;
-    m_seen = fmaxf(m_seen, m_t);
-    const bool over = __any(m_t > m_ref + kRebase);
+    m_seen = fmaxf(m_seen, mt);
+    const bool over = __any(mt > m_ref + kRebase);
     if (lane == 0) vote[4 * (ti & 1) + w] = over ? 1 : 0;
-    // P' = 2^(s - m_t) * 2^8 in fp8; the e8m0 B scale 2^(m_t - m_ref - 8) restores 2^(s - m_ref)
-    const float dm = fminf(fmaxf(m_t - m_ref, -160.f), 160.f);
-    const int pscale = min(max((int)dm - 8 + 127, 0), 254);
-    float psum = 0.f;
+    const float e0 = m0 == neg_inf() ? m_ref : m0, e1 = m1 == neg_inf() ? m_ref : m1;
+    const float d0 = fminf(fmaxf(e0 - m_ref, -160.f), 160.f), d1 = fminf(fmaxf(e1 - m_ref, -160.f), 160.f);
+    const int pscale = min(max((int)(hh ? d1 : d0) - 8 + 127, 0), 254);
+    // P'_u = 2^(c s - m_u + 8), fp8 hi + lo terms
+    float ps0 = 0.f, ps1 = 0.f;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      s0[r] = exp2f(s0[r] - m_t);
-      s1[r] = exp2f(s1[r] - m_t);
-      psum += s0[r] + s1[r];
+      s0[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[r], c, 8.f - e0));
+      s1[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[r], c, 8.f - e1));
+      ps0 += s0[r];
+      ps1 += s1[r];
     }
-    l_run += psum * exp2f(dm);
+    l_run += ps0 * __builtin_amdgcn_exp2f(d0 - 8.f) + ps1 * __builtin_amdgcn_exp2f(d1 - 8.f);
     // P'^T B operand: byte 16u + 4q + i <-> token 32u + 8q + 4hh + i; hi + lo fp8 terms
     v8i pbh, pbl;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       uint32_t h0, l0, h1, l1;
-      pack4_fp8_split(s0[4 * q] * kPScale, s0[4 * q + 1] * kPScale, s0[4 * q + 2] * kPScale,
-                      s0[4 * q + 3] * kPScale, h0, l0);
-      pack4_fp8_split(s1[4 * q] * kPScale, s1[4 * q + 1] * kPScale, s1[4 * q + 2] * kPScale,
-                      s1[4 * q + 3] * kPScale, h1, l1);
+      pack4_fp8_split(s0[4 * q], s0[4 * q + 1], s0[4 * q + 2], s0[4 * q + 3], h0, l0);
+      pack4_fp8_split(s1[4 * q], s1[4 * q + 1], s1[4 * q + 2], s1[4 * q + 3], h1, l1);
       pbh[q] = (int)h0;
       pbl[q] = (int)l0;
       pbh[4 + q] = (int)h1;
@@ -815,19 +836,26 @@ __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams 
       const v2i r3 = lds_read_tr8(vb + tr_off[3]);
       return v8i{r0[0], r0[1], r1[0], r1[1], r2[0], r2[1], r3[0], r3[1]};
     };
-    v8i avn = vfrag(0);
+    // dims in pairs of 32-row tiles so the hi and lo MFMAs of one accumulator
+    // are not back to back; one pair of fragments read ahead
+    v8i an0 = vfrag(0), an1 = vfrag(1);
 #pragma unroll
-    for (int dt = 0; dt < 16; ++dt) {
-      const v8i av = avn;
-      if (dt < 15) avn = vfrag(dt + 1);
-      o[dt] = mfma32_f8_bscale(av, pbh, pscale, o[dt]);
-      o[dt] = mfma32_f8_bscale(av, pbl, pscale, o[dt]);
+    for (int dt = 0; dt < 16; dt += 2) {
+      const v8i a0 = an0, a1 = an1;
+      if (dt < 14) {
+        an0 = vfrag(dt + 2);
+        an1 = vfrag(dt + 3);
+      }
+      o[dt] = mfma32_f8_bscale(a0, pbh, pscale, o[dt]);
+      o[dt + 1] = mfma32_f8_bscale(a1, pbh, pscale, o[dt + 1]);
+      o[dt] = mfma32_f8_bscale(a0, pbl, pscale, o[dt]);
+      o[dt + 1] = mfma32_f8_bscale(a1, pbl, pscale, o[dt + 1]);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
   if (!restart && ntiles > 0) {
     lds_barrier();  // the last tile's votes
-    restart = __builtin_amdgcn_readfirstlane(*reinterpret_cast<volatile uint32_t*>(vote + 4 * ((ntiles - 1) & 1))) != 0;
+    restart = __builtin_amdgcn_readfirstlane(*reinterpret_cast<const uint32_t*>(vote + 4 * ((ntiles - 1) & 1))) != 0;
   }
   if (!restart) break;
   // drain the ring (the prologue reuses it), then start over from m_ref = running max

@@ -88,6 +88,15 @@ __global__ void selftest_kernel(int which, const uint8_t* __restrict__ in, uint8
     if (which == 15) c = mfma16_f8_bscale(a, b, sc, c);
     else c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, sc, 0, 127);
     for (int r = 0; r < 4; ++r) D[(4 * (l / 16) + r) * 16 + (l % 16)] = c[r];
+  } else if (which == 19) {  // 32x32x64 fp8 with e8m0 scales on B: A [32][64], B [64][32], Sc [2][32]
+    const uint8_t* A = in;
+    const uint8_t* B = in + 2048;
+    const uint8_t* Sc = in + 4096;
+    v8i a, b;
+    for (int i = 0; i < 8; ++i) a[i] = *reinterpret_cast<const int*>(A + (l % 32) * 64 + 32 * (l / 32) + 4 * i);
+    for (int i = 0; i < 8; ++i) b[i] = (int)gather4(B, 32, 32 * (l / 32) + 4 * i, l % 32);
+    v16f c = mfma32_f8_bscale(a, b, Sc[(l / 32) * 32 + (l % 32)], v16f{});
+    for (int r = 0; r < 16; ++r) D[(8 * (r / 4) + 4 * (l / 32) + (r % 4)) * 32 + (l % 32)] = c[r];
   } else if (which == 4) {  // 16x16x32 fp8: A [16][32], B [32][16]
     const uint8_t* A = in;
     const uint8_t* B = in + 512;
@@ -226,7 +235,7 @@ hipError_t launch_selftest(int which, const void* in, void* out, hipStream_t str
                        static_cast<float*>(out));
     return hipGetLastError();
   }
-  if (which < 0 || (which > 10 && which != 15 && which != 16)) return hipErrorInvalidValue;
+  if (which < 0 || (which > 10 && which != 15 && which != 16 && which != 19)) return hipErrorInvalidValue;
   hipLaunchKernelGGL(selftest_kernel, dim3(1), dim3(64), 0, stream, which,
                      static_cast<const uint8_t*>(in), static_cast<uint8_t*>(out));
   return hipGetLastError();

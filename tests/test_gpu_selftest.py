@@ -11,7 +11,7 @@ pytestmark = pytest.mark.gpu
 
 
 IN_BYTES = {0: 4096, 1: 4096, 2: 3136, 3: 3136, 4: 1024, 5: 2048, 6: 1024, 7: 512, 8: 1024, 9: 1024,
-            10: 256, 11: 0, 12: 0, 13: 1024, 14: 1024, 15: 4160, 16: 4160, 17: 1024, 18: 1024}
+            10: 256, 11: 0, 12: 0, 13: 1024, 14: 1024, 15: 4160, 16: 4160, 17: 1024, 18: 1024, 19: 4160}
 
 
 def run(which, inp: np.ndarray, out_bytes: int) -> np.ndarray:
@@ -101,6 +101,23 @@ def test_mfma_block_scales(cuda, which):
         Af = Af * f.T
     ref = Af @ Bf
     scale = np.abs(Af) @ np.abs(Bf)
+    assert np.all(np.abs(D - ref) <= 1e-4 * scale), np.max(np.abs(D - ref) / scale)
+
+
+def test_mfma32_block_scales(cuda):
+    """32x32x64 fp8 with one e8m0 B scale per lane: byte j of lane group G
+    (G = l // 32) is K index 16G + (j & 15) + 32 (j >> 4), scaled by lane group
+    K // 32 = j >> 4 (operands loaded plain: lane group G, byte j = row 32G + j)."""
+    rng = np.random.default_rng(33)
+    A = fp8_codes(rng, (32, 64))
+    B = fp8_codes(rng, (64, 32))
+    Sc = rng.integers(120, 135, (2, 32)).astype(np.uint8)
+    D = run(19, np.concatenate([A.reshape(-1), B.reshape(-1), Sc.reshape(-1)]), 32 * 32 * 4)
+    D = D.view(np.float32).reshape(32, 32)
+    Af, Bf = O.e4m3fn_to_f32(A).astype(np.float64), O.e4m3fn_to_f32(B).astype(np.float64)
+    grp = np.array([(k % 32) >> 4 for k in range(64)])
+    ref = Af @ (Bf * np.exp2(Sc.astype(np.float64) - 127)[grp])
+    scale = np.abs(Af) @ np.abs(Bf * np.exp2(Sc.astype(np.float64) - 127)[grp])
     assert np.all(np.abs(D - ref) <= 1e-4 * scale), np.max(np.abs(D - ref) / scale)
 
 
