@@ -38,6 +38,21 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
+def measured_traffic(cid):
+    """HBM bytes per decode launch from the committed counter summary
+    (profiles/decode_hbm_traffic.md: FETCH_SIZE and WRITE_SIZE passes scaled by
+    a 256 MiB copy); None when the summary has no figure for this config."""
+    path = os.path.join(ROOT, "profiles", "decode_hbm_traffic.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith(f"traffic.config{cid}="):
+                    return int(line.split("=", 1)[1])
+    except OSError:
+        return None
+    return None
+
+
 def algorithmic(cfg, T):
     B, H, mode = cfg["batch"], cfg["num_heads"], cfg["kv_mode"]
     kv = T * (C_KV[mode] + 4)
@@ -165,6 +180,42 @@ def cpu_baseline(cid, data, budget_s):
                       f"scaled by token share x{scale:.2f}"}
 
 
+def profile_decode(cids, reps):
+    """Counter-collection driver (run under rocprofv3 --pmc): one 256 MiB copy
+    (the FETCH_SIZE / WRITE_SIZE calibration kernel), then per config one Q
+    quant + plan and `reps` decode launches, each after a 512 MiB flush."""
+    import torch
+
+    from amd_optimization_challenge_amd import inputs, ops
+
+    flush = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
+    src = torch.full((256 << 20,), 1, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    flush.zero_()
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    log("[profile] copy 256 MiB done")
+    del src, dst
+    for cid in cids:
+        data = inputs.generate_config(cid, device="cuda")
+        q, kv_data, _, kv_indptr, cfg = data
+        B, H, mode = q.shape[0], q.shape[1], cfg["kv_mode"]
+        ws = ops.workspace(B, H, mode, q.device)
+        qf8 = torch.empty(q.shape, dtype=torch.float8_e4m3fn, device=q.device)
+        qsc = torch.empty(1, dtype=torch.float32, device=q.device)
+        out = torch.empty((B, H, 512), dtype=torch.bfloat16, device=q.device)
+        ops.quant_fp8_per_tensor(q, qf8, qsc)
+        ops.plan(kv_indptr, B, H, mode, ws)
+        for _ in range(reps):
+            flush.zero_()
+            ops.decode(qf8, qsc, kv_data, kv_indptr, cfg["kv_indices"], H, cfg["sm_scale"], mode, ws, out)
+        torch.cuda.synchronize()
+        log(f"[profile] config {cid}: {reps} decode launches done")
+        del data, ws, out
+        torch.cuda.empty_cache()
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -174,6 +225,8 @@ def main(argv=None):
     ap.add_argument("--only-headline", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-budget-s", type=float, default=10.0)
+    ap.add_argument("--profile-decode", action="store_true",
+                    help="decode-only launches for counter collection (no JSON line)")
     args = ap.parse_args(argv)
     if args.gpus != 1:
         print(json.dumps({"error": "this operator runs on one GPU; multi-GPU sharding is design-only "
@@ -184,6 +237,9 @@ def main(argv=None):
     from amd_optimization_challenge_amd import _lib, inputs
 
     _lib.load()
+    if args.profile_decode:
+        profile_decode([args.config] if args.only_headline else sorted(inputs.CONFIGS), max(1, args.steps))
+        return 0
     flush = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
     cids = [args.config] if args.only_headline else sorted(inputs.CONFIGS)
     per = {}
@@ -220,7 +276,7 @@ def main(argv=None):
                    "total_kv": head["total_kv"], "page_size": 1, "permuted_pages": spec["permute"],
                    "sm_scale": inputs.SM_SCALE},
         "roofline": {"bound": "hbm", "achieved": head["decode_hbm_GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": head["decode_hbm_frac"], "traffic": None,
+                     "frac": head["decode_hbm_frac"], "traffic": measured_traffic(args.config),
                      "kernel": "decode (mla decode_h16/decode_h128)",
                      "bytes_per_launch": head["bytes_alg_decode"], "avg_launch_us": head["us_decode_kernel_mean"]},
         "cpu_baseline": cpu,
