@@ -81,11 +81,9 @@ int target_items_for(int batch, int num_heads, int kv_mode, int num_cu) {
 WsLayout workspace_layout(int batch, int num_heads, int kv_mode, int num_cu) {
   WsLayout L;
   L.target_items = target_items_for(batch, num_heads, kv_mode, num_cu);
-  // bound on max(target, batch) over every kv_mode, so the layout (which
-  // mla_combine recomputes without a mode) is mode-independent
-  int mi = 2 * batch > 2 * num_cu ? 2 * batch : 2 * num_cu;
-  mi = mi < 8 * num_cu ? mi : 8 * num_cu;
-  L.max_items = mi > batch ? mi : batch;
+  // the planner emits at most target + batch items; target does not depend on
+  // the kv mode, so mla_combine can recompute the layout without one
+  L.max_items = L.target_items + batch;
   int64_t off = 0;
   L.quant_off = off;
   off = align256(off + kQuantScratchBytes);

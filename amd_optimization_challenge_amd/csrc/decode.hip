@@ -204,12 +204,7 @@ __global__ __launch_bounds__(256, 1) void decode_h16_kernel(const DecodeParams p
       for (int j = 0; j < NJ; ++j) {
         const int i = tid + 256 * j;
         if (i < NV) {
-          const uint32_t wv[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
-          uint32_t o2[2] = {0, 0};
-#pragma unroll
-          for (int k = 0; k < 4; ++k)
-            o2[k >> 1] |= (quant_one(wv[k] & 0xFFFFu, qs) | (quant_one(wv[k] >> 16, qs) << 8)) << (16 * (k & 1));
-          *reinterpret_cast<uint2*>(qst + 8 * i) = make_uint2(o2[0], o2[1]);
+          *reinterpret_cast<uint2*>(qst + 8 * i) = quant8_fp8(xv[j], qs);
         }
       }
       lds_barrier();
@@ -911,38 +906,46 @@ __global__ __launch_bounds__(256) void combine_kernel(const DecodeParams p) {
   const int head = blockIdx.y * 16 + (threadIdx.x >> 4);
   const int d0 = blockIdx.z * 128 + (threadIdx.x & 15) * 8;
   const float* lse = p.part_lse + (int64_t)bi.x * H + head;
-  float M = neg_inf();
-  for (int s = 0; s < bi.y; ++s) M = fmaxf(M, lse[(int64_t)s * H]);
+  const float* po = p.part_o + ((int64_t)bi.x * H + head) * kVDim + d0;
+  const int64_t sstride = (int64_t)H * kVDim;
+  // one pass, 8 splits per batch: lse and partial loads of a batch are issued
+  // together; the running max rescales what is accumulated so far
+  float M = neg_inf(), wsum = 0.f;
   float acc[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = 0.f;
-  float wsum = 0.f;
-  if (M != neg_inf()) {
-    const float* po = p.part_o + ((int64_t)bi.x * H + head) * kVDim + d0;
-    const int64_t sstride = (int64_t)H * kVDim;
-    for (int s0 = 0; s0 < bi.y; s0 += 8) {
-      float4 v[8][2];
-      float wg[8];
+  for (int s0 = 0; s0 < bi.y; s0 += 8) {
+    float4 v[8][2];
+    float ls[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int s = min(s0 + j, bi.y - 1);
-        const float4* src = reinterpret_cast<const float4*>(po + s * sstride);
-        v[j][0] = src[0];
-        v[j][1] = src[1];
-        wg[j] = s0 + j < bi.y ? exp2f(lse[(int64_t)s * H] - M) : 0.f;
-      }
+    for (int j = 0; j < 8; ++j) {
+      const int s = min(s0 + j, bi.y - 1);
+      const float4* src = reinterpret_cast<const float4*>(po + s * sstride);
+      v[j][0] = src[0];
+      v[j][1] = src[1];
+      ls[j] = s0 + j < bi.y ? lse[(int64_t)s * H] : neg_inf();
+    }
+    float mb = M;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        wsum += wg[j];
-        acc[0] += wg[j] * v[j][0].x;
-        acc[1] += wg[j] * v[j][0].y;
-        acc[2] += wg[j] * v[j][0].z;
-        acc[3] += wg[j] * v[j][0].w;
-        acc[4] += wg[j] * v[j][1].x;
-        acc[5] += wg[j] * v[j][1].y;
-        acc[6] += wg[j] * v[j][1].z;
-        acc[7] += wg[j] * v[j][1].w;
-      }
+    for (int j = 0; j < 8; ++j) mb = fmaxf(mb, ls[j]);
+    if (mb == neg_inf()) continue;  // every piece so far is empty
+    const float r = M == neg_inf() ? 0.f : exp2f(M - mb);
+    wsum *= r;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] *= r;
+    M = mb;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float wg = exp2f(ls[j] - M);  // 0 for padding slots (lse -inf)
+      wsum += wg;
+      acc[0] += wg * v[j][0].x;
+      acc[1] += wg * v[j][0].y;
+      acc[2] += wg * v[j][0].z;
+      acc[3] += wg * v[j][0].w;
+      acc[4] += wg * v[j][1].x;
+      acc[5] += wg * v[j][1].y;
+      acc[6] += wg * v[j][1].z;
+      acc[7] += wg * v[j][1].w;
     }
   }
   const float inv = wsum > 0.f ? 1.0f / wsum : 0.f;

@@ -101,12 +101,13 @@ __device__ __forceinline__ float fp8_scale_from_amax(uint32_t amax_bits) {
   return bf16_bits_to_f32(f32_to_bf16_bits(a / 448.0f));
 }
 
-// y = e4m3fn(clamp(bf16(x / s), -448, 448)), reference.py:79-80
-__device__ __forceinline__ uint32_t quant_one(uint32_t h, float s) {
-  float y = bf16_bits_to_f32(f32_to_bf16_bits(bf16_bits_to_f32(h) / s));
-  y = fminf(fmaxf(y, -448.0f), 448.0f);
-  return f32_to_e4m3fn(y);
+// clamp(bf16(x / s), -448, 448) of reference.py:79-80, exact in f32
+__device__ __forceinline__ float quant_y(uint32_t h, float s) {
+  const float y = bf16_bits_to_f32(f32_to_bf16_bits(bf16_bits_to_f32(h) / s));
+  return fminf(fmaxf(y, -448.0f), 448.0f);
 }
+// y = e4m3fn(clamp(bf16(x / s), -448, 448)), reference.py:79-80
+__device__ __forceinline__ uint32_t quant_one(uint32_t h, float s) { return f32_to_e4m3fn(quant_y(h, s)); }
 
 // ---- wave helpers ------------------------------------------------------------
 __device__ __forceinline__ float shfl_xor_f(float v, int mask) {
@@ -155,6 +156,15 @@ __device__ __forceinline__ uint32_t pack4_fp8(float a, float b, float c, float d
   int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
   w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
   return (uint32_t)w;
+}
+// eight bf16 (one uint4) -> eight e4m3fn codes of the per-tensor quantizer; the
+// hardware convert rounds to nearest even like the reference cast, and after
+// the clamp to +-448 no input can overflow it
+__device__ __forceinline__ uint2 quant8_fp8(uint4 v, float s) {
+  return make_uint2(pack4_fp8(quant_y(v.x & 0xFFFFu, s), quant_y(v.x >> 16, s), quant_y(v.y & 0xFFFFu, s),
+                              quant_y(v.y >> 16, s)),
+                    pack4_fp8(quant_y(v.z & 0xFFFFu, s), quant_y(v.z >> 16, s), quant_y(v.w & 0xFFFFu, s),
+                              quant_y(v.w >> 16, s)));
 }
 
 // ---- LDS DMA (global_load_lds) and explicit waits --------------------------

@@ -88,16 +88,7 @@ __global__ __launch_bounds__(256) void quant_fp8_kernel(const uint16_t* __restri
   const uint4* xv = reinterpret_cast<const uint4*>(x);
   uint2* ov = reinterpret_cast<uint2*>(out);
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < nvec; i += (int64_t)gridDim.x * 256) {
-    uint4 v = xv[i];
-    uint32_t w[4] = {v.x, v.y, v.z, v.w};
-    uint32_t o[2] = {0, 0};
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      uint32_t lo = quant_one(w[k] & 0xFFFFu, s);
-      uint32_t hi = quant_one(w[k] >> 16, s);
-      o[k >> 1] |= (lo | (hi << 8)) << (16 * (k & 1));
-    }
-    ov[i] = make_uint2(o[0], o[1]);
+    ov[i] = quant8_fp8(xv[i], s);
   }
   for (int64_t i = (nvec << 3) + (int64_t)blockIdx.x * 256 + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * 256)
@@ -175,16 +166,18 @@ __global__ __launch_bounds__(256) void pack_mxfp4_kernel(const uint8_t* __restri
 
 // ---------------------------------------------------------------------------
 // split planner (one block of 256 threads)
-// chunk = the smallest multiple of 64 tokens for which the item count
-// sum_b max(1, ceil(L_b / chunk)) fits target_items (or the longest sequence,
-// if even one item per sequence exceeds it).  Sequence b is cut into
-// n_b = ceil(L_b / chunk) near-equal pieces (1 piece if empty).  Pieces of a
-// sequence are consecutive items; sequences are laid out longest piece first
-// (for batch <= 1024) so late-starting work-groups get the short items.  A
-// sequence with n_b == 1 writes its output directly (slot -1); otherwise each
-// piece owns partial slot = its item index.
+// Sequence b is cut into n_b = max(1, ceil(L_b / chunk)) near-equal pieces.
+// For batch <= 256, chunk = the smallest multiple of 64 with sum_b n_b <=
+// target_items (binary search from c0 = max(64, 64 ceil(T / (64 target))),
+// T = all tokens; the longest sequence if no chunk fits), and the sequences
+// are laid out longest piece first so late-starting work-groups get the short
+// items.  For larger batches chunk = c0 and the order is the sequence order.
+// Either way there are at most target_items + batch items (the workspace
+// bound).  Pieces of a sequence are consecutive items; a sequence with
+// n_b == 1 writes its output directly (slot -1); otherwise each piece owns
+// partial slot = its item index.
 // ---------------------------------------------------------------------------
-constexpr int kPlanSortMax = 1024;
+constexpr int kPlanSortMax = 256;
 
 __device__ long long block_sum_ll(long long v, long long* red) {
 #pragma unroll
@@ -195,140 +188,113 @@ __device__ long long block_sum_ll(long long v, long long* red) {
   return red[0] + red[1] + red[2] + red[3];
 }
 
-__device__ int block_max_i(int v, int* red) {
+// exclusive scan of one int per thread over the 256-thread block; *total =
+// the block sum (same in every thread)
+__device__ int block_exscan(int v, int* red, int* total) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  int x = v;
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = max(v, __shfl_xor(v, off, 64));
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(x, off, 64);
+    if (lane >= off) x += y;
+  }
+  __syncthreads();  // red free
+  if (lane == 63) red[w] = x;
   __syncthreads();
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-  __syncthreads();
-  return max(max(red[0], red[1]), max(red[2], red[3]));
+  int base = 0;
+  for (int i = 0; i < w; ++i) base += red[i];
+  *total = red[0] + red[1] + red[2] + red[3];
+  return base + x - v;
 }
 
 __device__ void build_plan(const int32_t* __restrict__ kv_indptr, int batch, int target_items,
                            int max_items, int32_t* __restrict__ plan) {
-  __shared__ long long s_red[4];
-  __shared__ int s_redi[4];
-  __shared__ int s_n[kPlanSortMax];  // item counts in layout order, then their exclusive scan
-  __shared__ int s_piece[kPlanSortMax];
-  __shared__ int s_scan[256];
-  __shared__ int s_carry;
-  __shared__ int s_len[kPlanSortMax];
-  __shared__ int s_rank[kPlanSortMax];
+  __shared__ long long s_redl[4];
+  __shared__ int s_red[4];
+  __shared__ int s_piece[kPlanSortMax];  // piece length per sequence
+  __shared__ int s_cnt[kPlanSortMax];    // item counts in layout order, then their exclusive scan
   const int tid = threadIdx.x;
-  const bool staged = batch <= kPlanSortMax;  // lengths kept in LDS
   long long tsum = 0;
-  int lmax = 0;
-  for (int b = tid; b < batch; b += 256) {
-    const int L = max(kv_indptr[b + 1] - kv_indptr[b], 0);
-    if (staged) s_len[b] = L;
-    tsum += L;
-    lmax = max(lmax, L);
-  }
-  auto len_of = [&](int b) { return staged ? s_len[b] : max(kv_indptr[b + 1] - kv_indptr[b], 0); };
-  const long long total = block_sum_ll(tsum, s_red);
-  lmax = block_max_i(lmax, s_redi);
-  // binary search on chunk / 64 in [1, ceil(lmax / 64)]
-  int lo = 1, hi = max(1, (lmax + kTile - 1) / kTile);
-  while (lo < hi) {
-    const int mid = (lo + hi) >> 1;
-    const long long c = (long long)mid * kTile;
-    long long cnt = 0;
-    for (int b = tid; b < batch; b += 256) {
-      const long long L = len_of(b);
-      cnt += L > 0 ? (L + c - 1) / c : 1;
+  for (int b = tid; b < batch; b += 256) tsum += max(kv_indptr[b + 1] - kv_indptr[b], 0);
+  const long long total = block_sum_ll(tsum, s_redl);
+  const long long per = (total + target_items - 1) / target_items;
+  long long chunk = max(64LL, (per + 63) / 64 * 64);
+  if (batch <= kPlanSortMax) {
+    // one sequence per thread: binary search on chunk / 64 in [c0 / 64, ceil(lmax / 64)]
+    const int Lt = tid < batch ? max(kv_indptr[tid + 1] - kv_indptr[tid], 0) : 0;
+    long long lm = Lt;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) lm = max(lm, (long long)__shfl_xor(lm, off, 64));
+    __syncthreads();
+    if ((tid & 63) == 0) s_redl[tid >> 6] = lm;
+    __syncthreads();
+    const long long lmax = max(max(s_redl[0], s_redl[1]), max(s_redl[2], s_redl[3]));
+    long long lo = chunk / 64, hi = max(lo, (lmax + 63) / 64);
+    while (lo < hi) {
+      const long long mid = (lo + hi) >> 1;
+      const long long c = mid * 64;
+      const long long cnt = block_sum_ll(tid < batch ? (Lt > 0 ? (Lt + c - 1) / c : 1) : 0, s_redl);
+      if (cnt <= target_items) hi = mid;
+      else lo = mid + 1;
     }
-    cnt = block_sum_ll(cnt, s_red);
-    if (cnt <= target_items) hi = mid;
-    else lo = mid + 1;
+    chunk = lo * 64;
   }
-  const long long chunk = (long long)lo * kTile;
+  auto len_of = [&](int b) { return max(kv_indptr[b + 1] - kv_indptr[b], 0); };
+  auto nb_of = [&](int L) { return L > 0 ? (int)((L + chunk - 1) / chunk) : 1; };
   int4* items = reinterpret_cast<int4*>(plan + kPlanHeader);
   int2* binfo = reinterpret_cast<int2*>(plan + kPlanHeader + 4 * max_items);
-  if (tid == 0) s_carry = 0;
-  __syncthreads();
+  auto emit = [&](int b, int L, int nb, int first) {
+    const int s0 = kv_indptr[b];
+    binfo[b] = make_int2(first, nb);
+    for (int i = 0; i < nb; ++i) {
+      const int t0 = s0 + (int)(((long long)i * L) / nb);
+      const int t1 = s0 + (int)(((long long)(i + 1) * L) / nb);
+      items[first + i] = make_int4(b, t0, t1, nb > 1 ? first + i : -1);
+    }
+  };
+  int carry = 0;
   if (batch <= kPlanSortMax) {
-    // piece length per sequence in LDS, then rank longest first (ties by index)
-    for (int b = tid; b < batch; b += 256) {
-      const int L = len_of(b);
-      const int nb = L > 0 ? (int)((L + chunk - 1) / chunk) : 1;
-      s_piece[b] = (L + nb - 1) / nb;
+    // rank sequences by piece length, longest first (ties by index)
+    const int b = tid;
+    int L = 0, nb = 0, piece = 0;
+    if (b < batch) {
+      L = len_of(b);
+      nb = nb_of(L);
+      piece = (L + nb - 1) / nb;
+      s_piece[b] = piece;
     }
     __syncthreads();
-    for (int b = tid; b < batch; b += 256) {
-      const int L = len_of(b);
-      const int nb = L > 0 ? (int)((L + chunk - 1) / chunk) : 1;
-      const int piece = s_piece[b];
-      int rank = 0;
+    int rank = 0;
+    if (b < batch) {
       for (int b2 = 0; b2 < batch; ++b2) {
         const int p2 = s_piece[b2];
         rank += (p2 > piece) || (p2 == piece && b2 < b);
       }
-      s_n[rank] = nb;
-      s_rank[b] = rank;
+      s_cnt[rank] = nb;
     }
     __syncthreads();
-    // exclusive scan of s_n in place, 256 at a time
-    for (int base = 0; base < batch; base += 256) {
-      const int i = base + tid;
-      const int v = i < batch ? s_n[i] : 0;
-      s_scan[tid] = v;
-      __syncthreads();
-      for (int off = 1; off < 256; off <<= 1) {
-        const int a = tid >= off ? s_scan[tid - off] : 0;
-        __syncthreads();
-        s_scan[tid] += a;
-        __syncthreads();
-      }
-      if (i < batch) s_n[i] = s_carry + s_scan[tid] - v;
-      __syncthreads();
-      if (tid == 255) s_carry += s_scan[255];
-      __syncthreads();
-    }
-    for (int b = tid; b < batch; b += 256) {
-      const int L = len_of(b);
-      const int first = s_n[s_rank[b]], nb = L > 0 ? (int)((L + chunk - 1) / chunk) : 1;
-      const int s0 = kv_indptr[b];
-      binfo[b] = make_int2(first, nb);
-      for (int i = 0; i < nb; ++i) {
-        const int t0 = s0 + (int)(((long long)i * L) / nb);
-        const int t1 = s0 + (int)(((long long)(i + 1) * L) / nb);
-        items[first + i] = make_int4(b, t0, t1, nb > 1 ? first + i : -1);
-      }
-    }
+    const int v = tid < batch ? s_cnt[tid] : 0;
+    const int ex = block_exscan(v, s_red, &carry);
+    __syncthreads();
+    if (tid < batch) s_cnt[tid] = ex;
+    __syncthreads();
+    if (b < batch) emit(b, L, nb, s_cnt[rank]);
   } else {
     for (int base = 0; base < batch; base += 256) {
       const int b = base + tid;
       int L = 0, nb = 0;
       if (b < batch) {
-        L = max(kv_indptr[b + 1] - kv_indptr[b], 0);
-        nb = L > 0 ? (int)((L + chunk - 1) / chunk) : 1;
+        L = len_of(b);
+        nb = nb_of(L);
       }
-      s_scan[tid] = nb;
-      __syncthreads();
-      for (int off = 1; off < 256; off <<= 1) {
-        const int a = tid >= off ? s_scan[tid - off] : 0;
-        __syncthreads();
-        s_scan[tid] += a;
-        __syncthreads();
-      }
-      const int first = s_carry + s_scan[tid] - nb;
-      if (b < batch) {
-        const int s0 = kv_indptr[b];
-        binfo[b] = make_int2(first, nb);
-        for (int i = 0; i < nb; ++i) {
-          const int t0 = s0 + (int)(((long long)i * L) / nb);
-          const int t1 = s0 + (int)(((long long)(i + 1) * L) / nb);
-          items[first + i] = make_int4(b, t0, t1, nb > 1 ? first + i : -1);
-        }
-      }
-      __syncthreads();
-      if (tid == 255) s_carry += s_scan[255];
-      __syncthreads();
+      int tot = 0;
+      const int ex = block_exscan(nb, s_red, &tot);
+      if (b < batch) emit(b, L, nb, carry + ex);
+      carry += tot;
     }
   }
-  __syncthreads();
   if (tid == 0) {
-    plan[0] = s_carry;
+    plan[0] = carry;
     plan[1] = (int)chunk;
     plan[2] = (int)total;
     plan[3] = batch;

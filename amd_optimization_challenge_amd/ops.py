@@ -225,7 +225,7 @@ def workspace_layout(batch: int, num_heads: int, kv_mode, num_cu: int) -> dict:
     mode = kv_mode_id(kv_mode)
     slots = num_cu  # one resident work-group per CU (the LDS ring fills the CU)
     target = min(max(slots, 2 * batch), 4 * slots)
-    max_items = max(min(max(2 * num_cu, 2 * batch), 8 * num_cu), batch)
+    max_items = target + batch
     off = 0
     lay = {"quant": off}
     off = _a256(off + QUANT_SCRATCH)

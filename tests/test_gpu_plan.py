@@ -30,9 +30,18 @@ def test_plan_covers_every_token_once(cuda, lens, heads, mode):
     torch.cuda.synchronize()
     P = ops.read_plan(ws, B, heads, mode)
     assert P["batch"] == B and P["total"] == sum(lens)
-    assert P["num_items"] <= P["max_items"] == P["layout"]["max_items"]
-    assert P["num_items"] <= max(P["layout"]["target_items"], B)
-    assert P["chunk"] % 64 == 0 and P["chunk"] >= 64
+    target = P["layout"]["target_items"]
+    assert P["num_items"] <= P["max_items"] == P["layout"]["max_items"] == target + B
+    # B <= 256: the smallest multiple of 64 (>= c0) whose piece count fits
+    # `target` (or the longest sequence); otherwise c0 = max(64, 64 ceil(T / (64 target)))
+    per = -(-sum(lens) // target)
+    c0 = max(64, -(-per // 64) * 64)
+    count = lambda c: sum(max(1, -(-L // c)) for L in lens)
+    if B <= 256:
+        cands = [c for c in range(c0, max(c0, -(-max(lens) // 64) * 64) + 1, 64) if count(c) <= target]
+        assert P["chunk"] == (cands[0] if cands else max(c0, -(-max(lens) // 64) * 64))
+    else:
+        assert P["chunk"] == c0
     items, binfo = P["items"].tolist(), P["batch_info"].tolist()
     for b in range(B):
         first, cnt = binfo[b]
@@ -47,13 +56,9 @@ def test_plan_covers_every_token_once(cuda, lens, heads, mode):
             assert it[2] - it[1] <= P["chunk"]
             assert it[3] == (-1 if cnt == 1 else first + j)
     assert sum(c for _, c in binfo) == P["num_items"]
-    # the chunk is minimal: one 64-token step smaller would need more items than allowed
-    if P["chunk"] > 64:
-        c = P["chunk"] - 64
-        need = sum(max(1, -(-L // c)) for L in lens)
-        assert need > P["layout"]["target_items"]
+    assert all(cnt == max(1, -(-L // P["chunk"])) for (_, cnt), L in zip(binfo, lens))
     # longest pieces first (sequences laid out by decreasing ceil(L / n))
-    if B <= 1024:
+    if B <= 256:
         order = sorted(range(B), key=lambda b: binfo[b][0])
         pieces = [-(-lens[b] // binfo[b][1]) for b in order]
         assert all(a >= c for a, c in zip(pieces, pieces[1:]))
