@@ -54,6 +54,13 @@ int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
 
 bool aligned(const void* p, int a) { return (reinterpret_cast<uintptr_t>(p) & (uintptr_t)(a - 1)) == 0; }
 
+int check_qlen(int batch, int q_seq_len) {
+  if (q_seq_len < 1 || batch % q_seq_len != 0)
+    return fail(MLA_ERR_INVALID_ARGUMENT, "q_seq_len must be >= 1 and divide the %d query rows (got %d)", batch,
+                q_seq_len);
+  return MLA_OK;
+}
+
 int check_shape(int batch, int num_heads, int kv_mode) {
   if (batch < 1) return fail(MLA_ERR_INVALID_ARGUMENT, "batch must be >= 1 (got %d)", batch);
   if (num_heads != 16 && num_heads != 128)
@@ -105,7 +112,8 @@ int decode_params(const void* q_fp8, const float* q_scale, const void* k_cache, 
                   const void* k_scales, int64_t k_scale_stride, const void* v_cache,
                   int64_t v_row_stride, const float* kv_scale, const int32_t* kv_indptr,
                   const int32_t* kv_indices, int batch, int num_heads, float sm_scale, int kv_mode,
-                  void* workspace, int64_t workspace_bytes, void* out, DecodeParams* p, WsLayout* L) {
+                  void* workspace, int64_t workspace_bytes, void* out, float* lse_out, DecodeParams* p,
+                  WsLayout* L) {
   int rc = check_shape(batch, num_heads, kv_mode);
   if (rc) return rc;
   int ncu = 0;
@@ -152,6 +160,7 @@ int decode_params(const void* q_fp8, const float* q_scale, const void* k_cache, 
   p->part_o = reinterpret_cast<float*>(ws + L->part_o_off);
   p->part_lse = reinterpret_cast<float*>(ws + L->part_lse_off);
   p->out = static_cast<uint16_t*>(out);
+  p->lse_out = lse_out;
   p->q_bf16 = nullptr;
   p->q_partials = nullptr;
   p->q_nparts = 0;
@@ -171,7 +180,7 @@ extern "C" {
 
 const char* mla_last_error(void) { return g_last_error.c_str(); }
 
-int mla_abi_version(void) { return 1; }
+int mla_abi_version(void) { return 2; }
 
 int mla_device_cu_count(int* num_cu) {
   if (!num_cu) return fail(MLA_ERR_INVALID_ARGUMENT, "num_cu is null");
@@ -200,8 +209,8 @@ int mla_quant_fp8_per_tensor(const void* x_bf16, int64_t n, void* out_fp8, float
   hipStream_t s = static_cast<hipStream_t>(stream);
   uint32_t* partials = static_cast<uint32_t*>(workspace);
   int nb = 0;
-  hipError_t e = launch_amax(static_cast<const uint16_t*>(x_bf16), n, partials, &nb, nullptr, nullptr, 0, 0,
-                             0, nullptr, s);
+  hipError_t e = launch_amax(static_cast<const uint16_t*>(x_bf16), n, partials, &nb, nullptr, nullptr, 0, 1,
+                             0, 0, nullptr, s);
   if (e != hipSuccess) return hip_fail(e, "amax launch");
   e = launch_quant_fp8(static_cast<const uint16_t*>(x_bf16), n, partials, nb,
                        static_cast<uint8_t*>(out_fp8), out_scale, s);
@@ -229,10 +238,11 @@ int mla_pack_mxfp4(const void* x_bf16, int64_t rows, int cols, int64_t x_row_str
   return MLA_OK;
 }
 
-int mla_plan(const int32_t* kv_indptr, int batch, int num_heads, int kv_mode, void* workspace,
+int mla_plan(const int32_t* kv_indptr, int batch, int q_seq_len, int num_heads, int kv_mode, void* workspace,
              int64_t workspace_bytes, void* stream) {
   int rc = check_shape(batch, num_heads, kv_mode);
   if (rc) return rc;
+  if ((rc = check_qlen(batch, q_seq_len))) return rc;
   if (!kv_indptr || !workspace) return fail(MLA_ERR_INVALID_ARGUMENT, "null pointer argument");
   if (!aligned(workspace, 256)) return fail(MLA_ERR_INVALID_ARGUMENT, "workspace must be 256-byte aligned");
   int ncu = 0;
@@ -242,7 +252,7 @@ int mla_plan(const int32_t* kv_indptr, int batch, int num_heads, int kv_mode, vo
     return fail(MLA_ERR_WORKSPACE_TOO_SMALL, "workspace needs %lld bytes (got %lld)", (long long)L.total,
                 (long long)workspace_bytes);
   int32_t* plan = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + L.plan_off);
-  hipError_t e = launch_plan(kv_indptr, batch, L.target_items, L.max_items, plan,
+  hipError_t e = launch_plan(kv_indptr, batch, q_seq_len, L.target_items, L.max_items, plan,
                              static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(e, "plan launch");
   return MLA_OK;
@@ -252,12 +262,12 @@ int mla_decode(const void* q_fp8, const float* q_scale, const void* k_cache, int
                const void* k_scales, int64_t k_scale_stride, const void* v_cache, int64_t v_row_stride,
                const float* kv_scale, const int32_t* kv_indptr, const int32_t* kv_indices, int batch,
                int num_heads, float sm_scale, int kv_mode, void* workspace, int64_t workspace_bytes,
-               void* out_bf16, void* stream) {
+               void* out_bf16, float* lse_out, void* stream) {
   DecodeParams p;
   WsLayout L;
   int rc = decode_params(q_fp8, q_scale, k_cache, k_row_stride, k_scales, k_scale_stride, v_cache,
                          v_row_stride, kv_scale, kv_indptr, kv_indices, batch, num_heads, sm_scale,
-                         kv_mode, workspace, workspace_bytes, out_bf16, &p, &L);
+                         kv_mode, workspace, workspace_bytes, out_bf16, lse_out, &p, &L);
   if (rc) return rc;
   hipError_t e = launch_decode(p, kv_mode, L.max_items, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(e, "decode launch");
@@ -265,7 +275,7 @@ int mla_decode(const void* q_fp8, const float* q_scale, const void* k_cache, int
 }
 
 int mla_combine(int batch, int num_heads, void* workspace, int64_t workspace_bytes, void* out_bf16,
-                void* stream) {
+                float* lse_out, void* stream) {
   int rc = check_shape(batch, num_heads, MLA_KV_FP8);
   if (rc) return rc;
   if (!workspace || !out_bf16) return fail(MLA_ERR_INVALID_ARGUMENT, "null pointer argument");
@@ -281,6 +291,7 @@ int mla_combine(int batch, int num_heads, void* workspace, int64_t workspace_byt
   p.part_o = reinterpret_cast<float*>(ws + L.part_o_off);
   p.part_lse = reinterpret_cast<float*>(ws + L.part_lse_off);
   p.out = static_cast<uint16_t*>(out_bf16);
+  p.lse_out = lse_out;
   p.batch = batch;
   p.num_heads = num_heads;
   p.max_items = L.max_items;
@@ -292,13 +303,14 @@ int mla_combine(int batch, int num_heads, void* workspace, int64_t workspace_byt
 int mla_decode_fwd(const void* q_bf16, const void* k_cache, int64_t k_row_stride, const void* k_scales,
                    int64_t k_scale_stride, const void* v_cache, int64_t v_row_stride,
                    const float* kv_scale, const int32_t* kv_indptr, const int32_t* kv_indices, int batch,
-                   int num_heads, float sm_scale, int kv_mode, void* workspace,
-                   int64_t workspace_bytes, void* out_bf16, void* stream) {
+                   int q_seq_len, int num_heads, float sm_scale, int kv_mode, void* workspace,
+                   int64_t workspace_bytes, void* out_bf16, float* lse_out, void* stream) {
   if (!q_bf16 || !aligned(q_bf16, 16)) return fail(MLA_ERR_INVALID_ARGUMENT, "q must be non-null and 16-byte aligned");
   if (!workspace) return fail(MLA_ERR_INVALID_ARGUMENT, "null workspace");
   char* ws = static_cast<char*>(workspace);
   int rc = check_shape(batch, num_heads, kv_mode);
   if (rc) return rc;
+  if ((rc = check_qlen(batch, q_seq_len))) return rc;
   int ncu = 0;
   if ((rc = cu_count(&ncu))) return rc;
   WsLayout L0 = workspace_layout(batch, num_heads, kv_mode, ncu);
@@ -311,15 +323,15 @@ int mla_decode_fwd(const void* q_bf16, const void* k_cache, int64_t k_row_stride
   WsLayout L;
   rc = decode_params(q_fp8, q_scale, k_cache, k_row_stride, k_scales, k_scale_stride, v_cache,
                      v_row_stride, kv_scale, kv_indptr, kv_indices, batch, num_heads, sm_scale, kv_mode,
-                     workspace, workspace_bytes, out_bf16, &p, &L);
+                     workspace, workspace_bytes, out_bf16, lse_out, &p, &L);
   if (rc) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t n = (int64_t)batch * num_heads * kQKDim;
   uint32_t* partials = reinterpret_cast<uint32_t*>(ws + L.quant_off);
   int nb = 0;
   hipError_t e = launch_amax(static_cast<const uint16_t*>(q_bf16), n, partials, &nb, kv_indptr,
-                             static_cast<const int32_t*>(kv_indices), batch, L.target_items, L.max_items,
-                             reinterpret_cast<int32_t*>(ws + L.plan_off), s);
+                             static_cast<const int32_t*>(kv_indices), batch, q_seq_len, L.target_items,
+                             L.max_items, reinterpret_cast<int32_t*>(ws + L.plan_off), s);
   if (e != hipSuccess) return hip_fail(e, "amax+plan launch");
   if (num_heads == 16) {
     // the H = 16 kernel quantizes its sequence's Q from the amax partials

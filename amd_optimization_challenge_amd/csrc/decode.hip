@@ -29,6 +29,7 @@
 namespace mla {
 
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kPScale = 256.0f;  // fp8 P = p * 256
 constexpr float kRebase = 96.0f;   // H128: max log2 distance of a tile max above the fixed reference
 
@@ -513,6 +514,8 @@ __global__ __launch_bounds__(256, 1) void decode_h16_kernel(const DecodeParams p
   const float inv = L > 0.f ? vscale / L : 0.f;
   const int head = l16;
   if (slot < 0) {
+    if (p.lse_out != nullptr && w == 0 && g == 0)
+      p.lse_out[(int64_t)b * 16 + head] = L > 0.f ? (m_ref + __log2f(L)) * kLn2 : neg_inf();
     uint16_t* orow = p.out + ((int64_t)b * 16 + head) * kVDim;
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
@@ -866,6 +869,8 @@ __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams 
   const float L = l_run + shfl_xor_f(l_run, 32);
   const float inv = L > 0.f ? vscale / L : 0.f;
   if (slot < 0) {
+    if (p.lse_out != nullptr && hh == 0)
+      p.lse_out[(int64_t)b * 128 + head] = L > 0.f ? (m_ref + __log2f(L)) * kLn2 : neg_inf();
     uint16_t* orow = p.out + ((int64_t)b * 128 + head) * kVDim;
 #pragma unroll
     for (int dt = 0; dt < 16; ++dt) {
@@ -949,6 +954,8 @@ __global__ __launch_bounds__(256) void combine_kernel(const DecodeParams p) {
     }
   }
   const float inv = wsum > 0.f ? 1.0f / wsum : 0.f;
+  if (p.lse_out != nullptr && blockIdx.z == 0 && (threadIdx.x & 15) == 0)
+    p.lse_out[(int64_t)b * H + head] = wsum > 0.f ? (M + __log2f(wsum)) * kLn2 : neg_inf();
   uint32_t w4[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i)

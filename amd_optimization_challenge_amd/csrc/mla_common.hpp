@@ -37,6 +37,7 @@ struct DecodeParams {
   float* part_o;             // [max_items, H, 512]
   float* part_lse;           // [max_items, H]  (log2 domain)
   uint16_t* out;             // [B, H, 512] bf16
+  float* lse_out;            // [B, H] natural-log lse, or nullptr
   // Q as bf16 with the per-tensor amax partials (the H = 16 kernel quantizes
   // its sequence's Q itself); q_fp8 / q_scale are used when q_bf16 is null
   const uint16_t* q_bf16;    // [B, H, 576] or nullptr

@@ -17,17 +17,17 @@ namespace mla {
 // pass 1: block-partial |x| max over bf16 (bit patterns: |x| ordering equals
 // unsigned ordering of (bits & 0x7fff) for non-NaN inputs)
 // ---------------------------------------------------------------------------
-__device__ void build_plan(const int32_t* __restrict__ kv_indptr, int batch, int target_items,
+__device__ void build_plan(const int32_t* __restrict__ kv_indptr, int batch, int qlen, int target_items,
                            int max_items, int32_t* __restrict__ plan);
 
 __global__ __launch_bounds__(256) void amax_kernel(const uint16_t* __restrict__ x, int64_t n,
                                                    uint32_t* __restrict__ partials, int nblocks,
                                                    const int32_t* __restrict__ kv_indptr,
                                                    const int32_t* __restrict__ kv_indices,
-                                                   int batch, int target_items, int max_items,
+                                                   int batch, int qlen, int target_items, int max_items,
                                                    int32_t* __restrict__ plan) {
   if ((int)blockIdx.x >= nblocks) {  // trailing block: split planner
-    build_plan(kv_indptr, batch, target_items, max_items, plan);
+    build_plan(kv_indptr, batch, qlen, target_items, max_items, plan);
     return;
   }
   if (kv_indices != nullptr) {
@@ -35,7 +35,7 @@ __global__ __launch_bounds__(256) void amax_kernel(const uint16_t* __restrict__ 
     // decode kernel's first slot fetches hit the caches (the decode reads
     // the indices a few microseconds later); the loaded values only feed a
     // store to a spare scratch word that nothing reads
-    const int64_t T = kv_indptr[batch];
+    const int64_t T = kv_indptr[batch / qlen];
     const int64_t lo = T * blockIdx.x / nblocks, hi = T * (blockIdx.x + 1) / nblocks;
     int acc = 0;
     for (int64_t i = (lo & ~31LL) + 32LL * threadIdx.x; i < hi; i += 32LL * 256) acc ^= kv_indices[i];
@@ -166,6 +166,11 @@ __global__ __launch_bounds__(256) void pack_mxfp4_kernel(const uint8_t* __restri
 
 // ---------------------------------------------------------------------------
 // split planner (one block of 256 threads)
+// Work is planned per query row: `batch` rows, q_seq_len = qlen rows per
+// sequence, row r = (sequence r / qlen, query i = r % qlen) attends to the
+// causal prefix of length L - (qlen - 1 - i) of its sequence (uniform-qo_len
+// causal decode, competitor_submissions/mi355x_reference/reference.py:188-193);
+// with qlen = 1 a row is a sequence.  Below, "sequence b" means row b.
 // Sequence b is cut into n_b = max(1, ceil(L_b / chunk)) near-equal pieces.
 // For batch <= 256, chunk = the smallest multiple of 64 with sum_b n_b <=
 // target_items (binary search from c0 = max(64, 64 ceil(T / (64 target))),
@@ -207,7 +212,16 @@ __device__ int block_exscan(int v, int* red, int* total) {
   return base + x - v;
 }
 
-__device__ void build_plan(const int32_t* __restrict__ kv_indptr, int batch, int target_items,
+// first key token and key count of query row r
+__device__ __forceinline__ int row_start(const int32_t* __restrict__ kv_indptr, int r, int qlen) {
+  return kv_indptr[r / qlen];
+}
+__device__ __forceinline__ int row_len(const int32_t* __restrict__ kv_indptr, int r, int qlen) {
+  const int b = r / qlen, i = r - b * qlen;
+  return max(kv_indptr[b + 1] - kv_indptr[b] - (qlen - 1 - i), 0);
+}
+
+__device__ void build_plan(const int32_t* __restrict__ kv_indptr, int batch, int qlen, int target_items,
                            int max_items, int32_t* __restrict__ plan) {
   __shared__ long long s_redl[4];
   __shared__ int s_red[4];
@@ -215,13 +229,13 @@ __device__ void build_plan(const int32_t* __restrict__ kv_indptr, int batch, int
   __shared__ int s_cnt[kPlanSortMax];    // item counts in layout order, then their exclusive scan
   const int tid = threadIdx.x;
   long long tsum = 0;
-  for (int b = tid; b < batch; b += 256) tsum += max(kv_indptr[b + 1] - kv_indptr[b], 0);
+  for (int b = tid; b < batch; b += 256) tsum += row_len(kv_indptr, b, qlen);
   const long long total = block_sum_ll(tsum, s_redl);
   const long long per = (total + target_items - 1) / target_items;
   long long chunk = max(64LL, (per + 63) / 64 * 64);
   if (batch <= kPlanSortMax) {
     // one sequence per thread: binary search on chunk / 64 in [c0 / 64, ceil(lmax / 64)]
-    const int Lt = tid < batch ? max(kv_indptr[tid + 1] - kv_indptr[tid], 0) : 0;
+    const int Lt = tid < batch ? row_len(kv_indptr, tid, qlen) : 0;
     long long lm = Lt;
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) lm = max(lm, (long long)__shfl_xor(lm, off, 64));
@@ -239,12 +253,12 @@ __device__ void build_plan(const int32_t* __restrict__ kv_indptr, int batch, int
     }
     chunk = lo * 64;
   }
-  auto len_of = [&](int b) { return max(kv_indptr[b + 1] - kv_indptr[b], 0); };
+  auto len_of = [&](int b) { return row_len(kv_indptr, b, qlen); };
   auto nb_of = [&](int L) { return L > 0 ? (int)((L + chunk - 1) / chunk) : 1; };
   int4* items = reinterpret_cast<int4*>(plan + kPlanHeader);
   int2* binfo = reinterpret_cast<int2*>(plan + kPlanHeader + 4 * max_items);
   auto emit = [&](int b, int L, int nb, int first) {
-    const int s0 = kv_indptr[b];
+    const int s0 = row_start(kv_indptr, b, qlen);
     binfo[b] = make_int2(first, nb);
     for (int i = 0; i < nb; ++i) {
       const int t0 = s0 + (int)(((long long)i * L) / nb);
@@ -302,10 +316,10 @@ __device__ void build_plan(const int32_t* __restrict__ kv_indptr, int batch, int
   }
 }
 
-__global__ __launch_bounds__(256) void plan_kernel(const int32_t* __restrict__ kv_indptr, int batch,
+__global__ __launch_bounds__(256) void plan_kernel(const int32_t* __restrict__ kv_indptr, int batch, int qlen,
                                                    int target_items, int max_items,
                                                    int32_t* __restrict__ plan) {
-  build_plan(kv_indptr, batch, target_items, max_items, plan);
+  build_plan(kv_indptr, batch, qlen, target_items, max_items, plan);
 }
 
 // ---------------------------------------------------------------------------
@@ -320,13 +334,13 @@ static int amax_blocks_for(int64_t n) {
 }
 
 hipError_t launch_amax(const uint16_t* x, int64_t n, uint32_t* partials, int* nblocks,
-                       const int32_t* kv_indptr, const int32_t* kv_indices, int batch, int target_items,
-                       int max_items, int32_t* plan, hipStream_t stream) {
+                       const int32_t* kv_indptr, const int32_t* kv_indices, int batch, int qlen,
+                       int target_items, int max_items, int32_t* plan, hipStream_t stream) {
   const int nb = amax_blocks_for(n);
   *nblocks = nb;
   const int grid = nb + (plan != nullptr ? 1 : 0);
   hipLaunchKernelGGL(amax_kernel, dim3(grid), dim3(256), 0, stream, x, n, partials, nb, kv_indptr,
-                     plan != nullptr ? kv_indices : nullptr, batch, target_items, max_items, plan);
+                     plan != nullptr ? kv_indices : nullptr, batch, qlen, target_items, max_items, plan);
   return hipGetLastError();
 }
 
@@ -354,9 +368,9 @@ hipError_t launch_pack_mxfp4(const uint16_t* x, int64_t rows, int cols, int64_t 
   return hipGetLastError();
 }
 
-hipError_t launch_plan(const int32_t* kv_indptr, int batch, int target_items, int max_items,
+hipError_t launch_plan(const int32_t* kv_indptr, int batch, int qlen, int target_items, int max_items,
                        int32_t* plan, hipStream_t stream) {
-  hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(256), 0, stream, kv_indptr, batch, target_items,
+  hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(256), 0, stream, kv_indptr, batch, qlen, target_items,
                      max_items, plan);
   return hipGetLastError();
 }

@@ -156,52 +156,65 @@ def _kv_args(kv_mode: int, kv_data: dict):
     raise ValueError(kv_mode)
 
 
-def plan(kv_indptr: torch.Tensor, batch: int, num_heads: int, kv_mode, ws: torch.Tensor) -> None:
+def plan(kv_indptr: torch.Tensor, batch: int, num_heads: int, kv_mode, ws: torch.Tensor,
+         q_seq_len: int = 1) -> None:
+    """``batch`` = query rows (sequences x q_seq_len)."""
     with torch.cuda.device(ws.device):
-        _lib.check(_lib.load().mla_plan(_ptr(kv_indptr), batch, num_heads, kv_mode_id(kv_mode), _ptr(ws),
-                                        ws.numel(), _stream()), "mla_plan")
+        _lib.check(_lib.load().mla_plan(_ptr(kv_indptr), batch, int(q_seq_len), num_heads, kv_mode_id(kv_mode),
+                                        _ptr(ws), ws.numel(), _stream()), "mla_plan")
 
 
-def decode(q_fp8, q_scale, kv_data, kv_indptr, kv_indices, num_heads, sm_scale, kv_mode, ws, out):
+def decode(q_fp8, q_scale, kv_data, kv_indptr, kv_indices, num_heads, sm_scale, kv_mode, ws, out, lse=None):
+    """One decode launch over the plan in ``ws``; rows = q_fp8.shape[0]."""
     mode = kv_mode_id(kv_mode)
     k, ks, ksc, kss, v, vs, sc = _kv_args(mode, kv_data)
-    batch = kv_indptr.numel() - 1
+    batch = q_fp8.shape[0]
     with torch.cuda.device(ws.device):
         _lib.check(_lib.load().mla_decode(
             _ptr(q_fp8), _ptr(q_scale), _ptr(k), ks, _ptr(ksc), kss, _ptr(v), vs, _ptr(sc),
             _ptr(kv_indptr), _ptr(kv_indices), batch, num_heads, float(sm_scale), mode, _ptr(ws),
-            ws.numel(), _ptr(out), _stream()), "mla_decode")
+            ws.numel(), _ptr(out), _ptr(lse), _stream()), "mla_decode")
 
 
-def combine(batch: int, num_heads: int, ws: torch.Tensor, out: torch.Tensor) -> None:
+def combine(batch: int, num_heads: int, ws: torch.Tensor, out: torch.Tensor, lse=None) -> None:
     with torch.cuda.device(ws.device):
-        _lib.check(_lib.load().mla_combine(batch, num_heads, _ptr(ws), ws.numel(), _ptr(out), _stream()),
-                   "mla_combine")
+        _lib.check(_lib.load().mla_combine(batch, num_heads, _ptr(ws), ws.numel(), _ptr(out), _ptr(lse),
+                                           _stream()), "mla_combine")
 
 
-def decode_fwd(q, kv_data, kv_indptr, kv_indices, sm_scale, kv_mode="fp8", out=None, ws=None):
-    """Whole operator: FP8-quantize q, plan, decode, combine.  q: bf16 [B, H, 576]."""
+def decode_fwd(q, kv_data, kv_indptr, kv_indices, sm_scale, kv_mode="fp8", out=None, ws=None, q_seq_len=1,
+               return_lse=False):
+    """Whole operator: FP8-quantize q, plan, decode, combine.
+
+    q: bf16 [rows, H, 576], rows = sequences x q_seq_len (row i of a sequence
+    attends causally to its first L - (q_seq_len - 1 - i) keys).  Returns the
+    bf16 [rows, H, 512] output, plus the f32 [rows, H] natural-log lse when
+    ``return_lse``.
+    """
     _require_cuda(q, kv_indptr, kv_indices)
     if q.dtype != torch.bfloat16 or q.dim() != 3 or q.shape[-1] != QK_DIM:
-        raise ValueError("q must be bf16 [batch, heads, 576]")
+        raise ValueError("q must be bf16 [rows, heads, 576]")
     if kv_indptr.dtype != torch.int32 or (kv_indices is not None and kv_indices.dtype != torch.int32):
         raise ValueError("kv_indptr / kv_indices must be int32")
     q = q.contiguous()
     batch, num_heads = q.shape[0], q.shape[1]
-    if kv_indptr.numel() != batch + 1:
-        raise ValueError(f"kv_indptr has {kv_indptr.numel()} entries, expected batch+1 = {batch + 1}")
+    q_seq_len = int(q_seq_len)
+    if q_seq_len < 1 or batch % q_seq_len != 0 or kv_indptr.numel() != batch // q_seq_len + 1:
+        raise ValueError(f"{batch} query rows, q_seq_len {q_seq_len} and {kv_indptr.numel()} kv_indptr "
+                         f"entries do not fit (need rows = sequences x q_seq_len, indptr = sequences + 1)")
     mode = kv_mode_id(kv_mode)
     k, ks, ksc, kss, v, vs, sc = _kv_args(mode, kv_data)
     if ws is None:
         ws = workspace(batch, num_heads, mode, q.device)
     if out is None:
         out = torch.empty((batch, num_heads, V_DIM), dtype=torch.bfloat16, device=q.device)
+    lse = torch.empty((batch, num_heads), dtype=torch.float32, device=q.device) if return_lse else None
     with torch.cuda.device(q.device):
         _lib.check(_lib.load().mla_decode_fwd(
             _ptr(q), _ptr(k), ks, _ptr(ksc), kss, _ptr(v), vs, _ptr(sc), _ptr(kv_indptr),
-            _ptr(kv_indices), batch, num_heads, float(sm_scale), mode, _ptr(ws), ws.numel(), _ptr(out),
-            _stream()), "mla_decode_fwd")
-    return out
+            _ptr(kv_indices), batch, q_seq_len, num_heads, float(sm_scale), mode, _ptr(ws), ws.numel(),
+            _ptr(out), _ptr(lse), _stream()), "mla_decode_fwd")
+    return (out, lse) if return_lse else out
 
 
 def selftest(which: int, inp: torch.Tensor, out: torch.Tensor) -> None:

@@ -6,8 +6,13 @@ Mirrors mixed-mla/submission.py:626-644: same ``data`` tuple, same
 HIP pipeline (FP8 Q quant -> on-device split plan -> decode -> LSE combine)
 from libmla_mi355x.so, and it honours ``config["sm_scale"]`` (the reference
 ignores it, mixed-mla/submission.py:37) plus the optional ``num_heads``,
-``kv_indices`` and ``kv_mode`` keys.  There is no fallback: a missing library
-or an unsupported shape raises.
+``kv_indices`` and ``kv_mode`` keys.  ``config["q_seq_len"] > 1`` runs the
+reference's causal multi-token decode (uniform qo length,
+competitor_submissions/mi355x_reference/reference.py:188-193; ``qo_indptr``
+is taken to be ``arange * q_seq_len`` as generate_input makes it, :330), and
+``config["return_lse"]`` also returns the f32 log-sum-exp
+(mixed-mla/asm_dumps/aiter_mla.py:367-371).  There is no fallback: a missing
+library or an unsupported shape raises.
 """
 from __future__ import annotations
 
@@ -24,14 +29,15 @@ DEFAULT_SM_SCALE = 1.0 / math.sqrt(576.0)
 def custom_kernel(data: input_t) -> output_t:
     q, kv_data, qo_indptr, kv_indptr, config = data
     q_seq_len = int(config.get("q_seq_len", 1))
-    if q_seq_len != 1:
-        raise NotImplementedError("only decode (q_seq_len == 1) is implemented")
     num_heads = q.shape[1]
     if int(config.get("num_heads", num_heads)) != num_heads:
         raise ValueError("config['num_heads'] does not match q.shape[1]")
     sm_scale = float(config.get("sm_scale", DEFAULT_SM_SCALE))
     kv_mode = config.get("kv_mode", "fp8")
     kv_indices = config.get("kv_indices")
-    if q.shape[0] != kv_indptr.numel() - 1:
-        raise ValueError("q.shape[0] must equal batch (q_seq_len == 1)")
-    return ops.decode_fwd(q, kv_data, kv_indptr, kv_indices, sm_scale, kv_mode)
+    if q.shape[0] != (kv_indptr.numel() - 1) * q_seq_len:
+        raise ValueError("q.shape[0] must equal batch * q_seq_len")
+    if qo_indptr is not None and qo_indptr.numel() != kv_indptr.numel():
+        raise ValueError("qo_indptr and kv_indptr must both have batch + 1 entries")
+    return ops.decode_fwd(q, kv_data, kv_indptr, kv_indices, sm_scale, kv_mode, q_seq_len=q_seq_len,
+                          return_lse=bool(config.get("return_lse", False)))

@@ -8,16 +8,24 @@
  * calling thread.  All device memory is caller-owned; scratch lives in the
  * caller-provided workspace whose size `mla_workspace_bytes` reports.
  *
- * Layouts (row-major, byte strides given in bytes):
- *   q            [batch, num_heads, 576]  bf16          (q_seq_len = 1)
+ * `batch` counts query rows: sequences x q_seq_len, the q_seq_len rows of a
+ * sequence consecutive.  Row i of a sequence with L keys attends to its first
+ * L - (q_seq_len - 1 - i) keys (the uniform-qo_len causal decode of
+ * competitor_submissions/mi355x_reference/reference.py:188-193); q_seq_len = 1
+ * is plain decode.
+ *
+ * Layouts (row-major, byte strides given in bytes), S = batch / q_seq_len:
+ *   q            [batch, num_heads, 576]  bf16
  *   q_fp8        [batch, num_heads, 576]  float8 e4m3fn (OCP)
  *   fp8 cache    [slots, 576]             e4m3fn, one per-tensor f32 scale
  *   mxfp4 cache  [slots, 288]             e2m1 pairs, low nibble = even element
  *   mxfp4 scales [slots, scale_stride]    e8m0, first 18 used (stride >= 18)
- *   kv_indptr    [batch + 1]              int32, token offsets into kv_indices
- *   kv_indices   [kv_indptr[batch]]       int32 cache slot per token (page size 1);
+ *   kv_indptr    [S + 1]                  int32, token offsets into kv_indices
+ *   kv_indices   [kv_indptr[S]]           int32 cache slot per token (page size 1);
  *                                         NULL means identity (slot = offset)
  *   out          [batch, num_heads, 512]  bf16
+ *   lse_out      [batch, num_heads]       f32 ln sum exp(scores), optional (NULL =
+ *                                         not written); -inf for a row with no keys
  *
  * References below are path:line in dorhuri123/AMD_optimization_challenge.
  */
@@ -45,7 +53,7 @@ extern "C" {
 /* Message describing the last failure on this thread ("" if none). */
 const char* mla_last_error(void);
 
-/* ABI version, bumped on any signature change. */
+/* ABI version, bumped on any signature change (2: q_seq_len, lse_out). */
 int mla_abi_version(void);
 
 /* Number of compute units on the current device (used by the split planner). */
@@ -84,10 +92,11 @@ int mla_pack_mxfp4(const void* x_bf16, int64_t rows, int cols, int64_t x_row_str
  * Split-KV work partition, computed on the device from kv_indptr (no host
  * sync).  Replaces get_mla_metadata_v1
  * (competitor_submissions/mi355x_reference/reference.py:161-209) and the
- * uniform cdiv split of mixed-mla/submission.py:158-160.  The plan lives in the
- * workspace and is consumed by mla_decode / mla_combine.
+ * uniform cdiv split of mixed-mla/submission.py:158-160; q_seq_len is the
+ * reference's max_seqlen_qo with is_causal (reference.py:188-193).  The plan
+ * lives in the workspace and is consumed by mla_decode / mla_combine.
  */
-int mla_plan(const int32_t* kv_indptr, int batch, int num_heads, int kv_mode,
+int mla_plan(const int32_t* kv_indptr, int batch, int q_seq_len, int num_heads, int kv_mode,
              void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
@@ -99,33 +108,38 @@ int mla_plan(const int32_t* kv_indptr, int batch, int num_heads, int kv_mode,
  *   mxfp4 K : k_cache = packed cache (row stride >= 288), k_scales = e8m0
  *   fp8 V   : v_cache = fp8 cache (row stride >= 512), kv_scale = its scale
  *   mxfp4 V : same rows as K (v_cache ignored)
- * Scores are (q_fp8*q_scale).(k*k_scale) * sm_scale.
+ * Scores are (q_fp8*q_scale).(k*k_scale) * sm_scale.  lse_out (optional) gets
+ * the rows written here, as mla_decode_fwd's return_lse
+ * (mixed-mla/asm_dumps/aiter_mla.py:367-371).
  */
 int mla_decode(const void* q_fp8, const float* q_scale, const void* k_cache,
                int64_t k_row_stride, const void* k_scales, int64_t k_scale_stride,
                const void* v_cache, int64_t v_row_stride, const float* kv_scale,
                const int32_t* kv_indptr, const int32_t* kv_indices, int batch,
                int num_heads, float sm_scale, int kv_mode, void* workspace,
-               int64_t workspace_bytes, void* out_bf16, void* stream);
+               int64_t workspace_bytes, void* out_bf16, float* lse_out, void* stream);
 
 /*
  * Log-sum-exp merge of the split partials of every split sequence into `out`
- * (bf16).  Replaces mla_reduce_v1 (mixed-mla/asm_dumps/aiter_mla.py:421-430).
+ * (bf16), and their lse into lse_out when it is not NULL.  Replaces
+ * mla_reduce_v1 (mixed-mla/asm_dumps/aiter_mla.py:421-430).
  */
 int mla_combine(int batch, int num_heads, void* workspace, int64_t workspace_bytes,
-                void* out_bf16, void* stream);
+                void* out_bf16, float* lse_out, void* stream);
 
 /*
  * The whole operator: quantize q (bf16) to FP8, plan, decode, combine.  This is
- * the C side of custom_kernel(data) (mixed-mla/submission.py:626-644) for
- * q_seq_len = 1; the per-step entry points above are its stages.
+ * the C side of custom_kernel(data) (mixed-mla/submission.py:626-644) and of
+ * AITER's mla_decode_fwd (mixed-mla/asm_dumps/aiter_mla.py:149-175) with
+ * max_seqlen_q = q_seq_len and return_lse = (lse_out != NULL); the per-step
+ * entry points above are its stages.
  */
 int mla_decode_fwd(const void* q_bf16, const void* k_cache, int64_t k_row_stride,
                    const void* k_scales, int64_t k_scale_stride, const void* v_cache,
                    int64_t v_row_stride, const float* kv_scale,
                    const int32_t* kv_indptr, const int32_t* kv_indices, int batch,
-                   int num_heads, float sm_scale, int kv_mode, void* workspace,
-                   int64_t workspace_bytes, void* out_bf16, void* stream);
+                   int q_seq_len, int num_heads, float sm_scale, int kv_mode, void* workspace,
+                   int64_t workspace_bytes, void* out_bf16, float* lse_out, void* stream);
 
 /*
  * Diagnostics (no counterpart in the reference): runs one wave of a built-in

@@ -289,12 +289,33 @@ def dequant_kv(kv_mode: str, fp8_codes=None, fp8_scale=None, fp4_packed=None,
     raise ValueError(kv_mode)
 
 
-def mla_decode(q_deq, k_deq, v_deq, kv_indptr, kv_indices, sm_scale, threads=None):
-    """out[b,h,:] = softmax(q[b,h] . K[idx_b]^T * sm_scale) V[idx_b], float32.
+def row_ranges(kv_indptr, q_seq_len=1):
+    """(start, length) of the keys each query row attends to.
 
-    q_deq [B,H,576] f32; k_deq [T,576]; v_deq [T,512]; kv_indices maps each
-    logical token to a cache row (page size 1).  An empty sequence yields 0.
-    Computed with torch on the CPU (batched fp32 GEMM), one sequence at a time.
+    Rows are (sequence b, query i) in order, q_seq_len per sequence; query i
+    sees the causal prefix of length L_b - (q_seq_len - 1 - i) (clamped at 0):
+    the uniform-qo_len causal decode of competitor_submissions/mi355x_reference/
+    reference.py:188-193 (is_causal=True, uni_seqlen_qo=q_seq_len).  With
+    q_seq_len = 1 this is simply [indptr[b], indptr[b+1]).
+    """
+    indptr = np.asarray(kv_indptr, dtype=np.int64)
+    out = []
+    for b in range(len(indptr) - 1):
+        L = int(indptr[b + 1] - indptr[b])
+        for i in range(q_seq_len):
+            out.append((int(indptr[b]), max(L - (q_seq_len - 1 - i), 0)))
+    return out
+
+
+def mla_decode(q_deq, k_deq, v_deq, kv_indptr, kv_indices, sm_scale, threads=None, q_seq_len=1,
+               return_lse=False):
+    """out[r,h,:] = softmax(q[r,h] . K[keys_r]^T * sm_scale) V[keys_r], float32.
+
+    q_deq [rows,H,576] f32 with rows = sequences * q_seq_len; k_deq [T,576];
+    v_deq [T,512]; kv_indices maps each logical token to a cache row (page
+    size 1); keys_r as in row_ranges.  A row with no keys yields 0 (and
+    lse -inf).  With return_lse, also lse[r,h] = ln sum exp(sm_scale q.k)
+    (natural log).  Computed with torch on the CPU (fp32 GEMM), one row at a time.
     """
     import torch
 
@@ -303,53 +324,62 @@ def mla_decode(q_deq, k_deq, v_deq, kv_indptr, kv_indices, sm_scale, threads=Non
     q = torch.as_tensor(np.ascontiguousarray(q_deq), dtype=torch.float32)
     k = torch.as_tensor(np.ascontiguousarray(k_deq), dtype=torch.float32)
     v = torch.as_tensor(np.ascontiguousarray(v_deq), dtype=torch.float32)
-    indptr = np.asarray(kv_indptr, dtype=np.int64)
     idx = torch.as_tensor(np.asarray(kv_indices, dtype=np.int64))
-    B, H, _ = q.shape
-    out = torch.zeros((B, H, V_DIM), dtype=torch.float32)
-    for b in range(B):
-        s0, s1 = int(indptr[b]), int(indptr[b + 1])
-        if s1 <= s0:
+    R, H, _ = q.shape
+    ranges = row_ranges(kv_indptr, q_seq_len)
+    assert len(ranges) == R, "q rows must equal sequences * q_seq_len"
+    out = torch.zeros((R, H, V_DIM), dtype=torch.float32)
+    lse = torch.full((R, H), float("-inf"), dtype=torch.float32)
+    for r, (s0, n) in enumerate(ranges):
+        if n <= 0:
             continue
-        rows = idx[s0:s1]
+        rows = idx[s0:s0 + n]
         kb = k.index_select(0, rows)
         vb = v.index_select(0, rows)
-        s = (q[b] @ kb.T) * float(sm_scale)
+        s = (q[r] @ kb.T) * float(sm_scale)
         p = torch.softmax(s, dim=-1)
-        out[b] = p @ vb
-    return out.numpy()
+        out[r] = p @ vb
+        lse[r] = torch.logsumexp(s, dim=-1)
+    return (out.numpy(), lse.numpy()) if return_lse else out.numpy()
 
 
-def mla_decode_f64(q_deq, k_deq, v_deq, kv_indptr, kv_indices, sm_scale):
+def mla_decode_f64(q_deq, k_deq, v_deq, kv_indptr, kv_indices, sm_scale, q_seq_len=1, return_lse=False):
     """Float64 pure-numpy brute force (small shapes only), explicit max-shifted softmax."""
     q = np.asarray(q_deq, np.float64)
-    B, H, _ = q.shape
-    out = np.zeros((B, H, V_DIM), np.float64)
-    for b in range(B):
-        s0, s1 = int(kv_indptr[b]), int(kv_indptr[b + 1])
+    R, H, _ = q.shape
+    out = np.zeros((R, H, V_DIM), np.float64)
+    lse = np.full((R, H), -np.inf)
+    for r, (s0, n) in enumerate(row_ranges(kv_indptr, q_seq_len)):
         for h in range(H):
-            if s1 <= s0:
+            if n <= 0:
                 continue
-            rows = np.asarray(kv_indices[s0:s1], np.int64)
-            sc = np.array([np.dot(q[b, h], np.asarray(k_deq[r], np.float64)) for r in rows]) * sm_scale
-            w = np.exp(sc - sc.max())
+            rows = np.asarray(kv_indices[s0:s0 + n], np.int64)
+            sc = np.array([np.dot(q[r, h], np.asarray(k_deq[t], np.float64)) for t in rows]) * sm_scale
+            mx = sc.max()
+            w = np.exp(sc - mx)
+            lse[r, h] = mx + np.log(w.sum())
             w /= w.sum()
-            out[b, h] = sum(w[i] * np.asarray(v_deq[r], np.float64) for i, r in enumerate(rows))
-    return out
+            out[r, h] = sum(w[i] * np.asarray(v_deq[t], np.float64) for i, t in enumerate(rows))
+    return (out, lse) if return_lse else out
 
 
-def reference_path(q_bits, kv_mode, caches, kv_indptr, kv_indices, sm_scale, threads=None):
+def reference_path(q_bits, kv_mode, caches, kv_indptr, kv_indices, sm_scale, threads=None, q_seq_len=1,
+                   return_lse=False):
     """The full CPU restatement of the reference path for one decode call.
 
     quantize Q (a2) -> dequantize Q and KV -> fp32 attention -> bf16 bits.
     ``caches`` = dict(fp8_codes, fp8_scale, fp4_packed, fp4_scales) (numpy).
-    Returns (out_bf16_bits [B,H,512], out_f32).
+    Returns (out_bf16_bits [rows,H,512], out_f32[, lse [rows,H] natural log]).
     """
     qc, qs = quantize_fp8_per_tensor(q_bits)
     q_deq = dequant_fp8(qc, qs)
     k, v = dequant_kv(kv_mode, **caches)
-    out = mla_decode(q_deq, k, v, kv_indptr, kv_indices, sm_scale, threads=threads)
-    return f32_to_bf16(out), out
+    res = mla_decode(q_deq, k, v, kv_indptr, kv_indices, sm_scale, threads=threads, q_seq_len=q_seq_len,
+                     return_lse=return_lse)
+    if return_lse:
+        out, lse = res
+        return f32_to_bf16(out), out, lse
+    return f32_to_bf16(res), res
 
 
 def time_reference_path(q_bits, kv_mode, caches, kv_indptr, kv_indices, sm_scale,

@@ -26,7 +26,7 @@ def test_library_exports_every_declared_symbol():
     lib = _lib.load()
     for name in declared_symbols():
         assert hasattr(lib, name), name
-    assert lib.mla_abi_version() == 1
+    assert lib.mla_abi_version() == 2
 
 
 def test_argument_errors_without_device():
@@ -42,6 +42,10 @@ def test_argument_errors_without_device():
     assert lib.mla_selftest(0, None, None, None) == _lib.MLA_ERR_INVALID_ARGUMENT
     with pytest.raises(_lib.MlaLibraryError):
         _lib.check(lib.mla_workspace_bytes(4, 24, 0, ctypes.byref(n)), "mla_workspace_bytes")
+    # q_seq_len must divide the query rows (checked before any device call)
+    assert lib.mla_plan(None, 6, 4, 16, 0, None, 0, None) == _lib.MLA_ERR_INVALID_ARGUMENT
+    assert lib.mla_decode_fwd(None, None, 576, None, 0, None, 0, None, None, None, 6, 4, 16, 0.1, 0, None, 0,
+                              None, None, None) == _lib.MLA_ERR_INVALID_ARGUMENT
 
 
 def test_custom_kernel_rejects_unsupported_configs_before_launch():
@@ -51,7 +55,7 @@ def test_custom_kernel_rejects_unsupported_configs_before_launch():
 
     q = torch.zeros((2, 16, 576), dtype=torch.bfloat16)
     indptr = torch.tensor([0, 1, 2], dtype=torch.int32)
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(ValueError):  # 2 query rows cannot be 2 sequences x q_seq_len 2
         custom_kernel((q, {}, indptr, indptr, {"q_seq_len": 2}))
     with pytest.raises(ValueError):
         custom_kernel((q, {}, indptr, indptr, {"num_heads": 128}))

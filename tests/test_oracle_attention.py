@@ -84,3 +84,40 @@ def test_reference_path_end_to_end_small():
         ref = O.mla_decode(qf, kf, kf[:, :512], indptr, idx, 1 / np.sqrt(192))
         err = np.linalg.norm(f - ref) / np.linalg.norm(ref)
         assert err < (0.06 if mode == "fp8" else 0.25), (mode, err)
+
+
+# ---- q_seq_len > 1 (causal MTP rows) and the log-sum-exp output -------------
+def test_lse_matches_float64_and_closed_form():
+    rng = np.random.default_rng(11)
+    q, k, v, indptr, idx = rand_case(rng, 3, 2, [6, 1, 0])
+    sm = 0.2
+    out, lse = O.mla_decode(q, k, v, indptr, idx, sm, return_lse=True)
+    ref, ref_lse = O.mla_decode_f64(q, k, v, indptr, idx, sm, return_lse=True)
+    np.testing.assert_allclose(out, ref, rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(lse[:2], ref_lse[:2], rtol=1e-5, atol=1e-4)
+    # one key: lse = sm * q.k exactly; no key: -inf
+    np.testing.assert_allclose(lse[1], sm * (q[1] @ k[idx[6]]), rtol=1e-5, atol=1e-4)
+    assert np.all(np.isneginf(lse[2]))
+
+
+@pytest.mark.parametrize("qlen", [2, 4])
+def test_mtp_rows_are_causal_prefix_decodes(qlen):
+    """Query i of a sequence with L keys equals a single-query decode over the
+    first L - (qlen - 1 - i) keys (a separate call on a truncated indptr)."""
+    rng = np.random.default_rng(20 + qlen)
+    lens = [9, 3, 1, 17]
+    S = len(lens)
+    q, k, v, indptr, idx = rand_case(rng, S * qlen, 2, [0] * S * qlen, T_extra=sum(lens) + 3)
+    indptr = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    idx = rng.permutation(k.shape[0])[: indptr[-1]]
+    out, lse = O.mla_decode(q, k, v, indptr, idx, 0.15, q_seq_len=qlen, return_lse=True)
+    ref, ref_lse = O.mla_decode_f64(q, k, v, indptr, idx, 0.15, q_seq_len=qlen, return_lse=True)
+    np.testing.assert_allclose(out, ref, rtol=1e-5, atol=1e-5)
+    for b in range(S):
+        for i in range(qlen):
+            n = max(lens[b] - (qlen - 1 - i), 0)
+            one = O.mla_decode(q[b * qlen + i: b * qlen + i + 1], k, v, np.array([0, n]),
+                               idx[indptr[b]: indptr[b] + n], 0.15)
+            np.testing.assert_allclose(out[b * qlen + i], one[0], rtol=1e-6, atol=1e-6)
+            if n == 0:
+                assert np.all(out[b * qlen + i] == 0) and np.all(np.isneginf(lse[b * qlen + i]))
