@@ -238,6 +238,39 @@ int mla_pack_mxfp4(const void* x_bf16, int64_t rows, int cols, int64_t x_row_str
   return MLA_OK;
 }
 
+int mla_append_kv(const void* x_bf16, int64_t n, int64_t x_row_stride, const int32_t* slots,
+                  void* fp8_cache, int64_t fp8_row_stride, const float* fp8_scale, void* fp4_cache,
+                  int64_t fp4_row_stride, void* fp4_scales, int64_t fp4_scale_stride, uint32_t* amax_out,
+                  void* stream) {
+  if (n < 0 || n > kAppendMaxTokens)
+    return fail(MLA_ERR_INVALID_ARGUMENT, "n must be in [0, %lld] (got %lld)", (long long)kAppendMaxTokens,
+                (long long)n);
+  if (!fp8_cache && !fp4_cache) return fail(MLA_ERR_INVALID_ARGUMENT, "no cache to write (both NULL)");
+  if (n == 0) return MLA_OK;
+  if (!x_bf16) return fail(MLA_ERR_INVALID_ARGUMENT, "null pointer argument");
+  if (x_row_stride < 2LL * kQKDim || (x_row_stride % 16) != 0 || !aligned(x_bf16, 16))
+    return fail(MLA_ERR_INVALID_ARGUMENT, "x rows must be 16-byte aligned with stride >= 1152 bytes");
+  if (fp8_cache) {
+    if (!fp8_scale) return fail(MLA_ERR_INVALID_ARGUMENT, "fp8_cache needs fp8_scale");
+    if (fp8_row_stride < kQKDim || (fp8_row_stride % 16) != 0 || !aligned(fp8_cache, 16))
+      return fail(MLA_ERR_INVALID_ARGUMENT, "fp8 cache rows must be 16-byte aligned with stride >= 576");
+  }
+  if (fp4_cache) {
+    if (!fp4_scales) return fail(MLA_ERR_INVALID_ARGUMENT, "fp4_cache needs fp4_scales");
+    if (fp4_row_stride < kFp4RowBytes || (fp4_row_stride % 16) != 0 || !aligned(fp4_cache, 16))
+      return fail(MLA_ERR_INVALID_ARGUMENT, "mxfp4 cache rows must be 16-byte aligned with stride >= 288");
+    if (fp4_scale_stride < kMxBlocks)
+      return fail(MLA_ERR_INVALID_ARGUMENT, "fp4_scale_stride must be >= 18");
+  }
+  hipError_t e = launch_append_kv(static_cast<const uint16_t*>(x_bf16), n, x_row_stride, slots,
+                                  static_cast<uint8_t*>(fp8_cache), fp8_row_stride, fp8_scale,
+                                  static_cast<uint8_t*>(fp4_cache), fp4_row_stride,
+                                  static_cast<uint8_t*>(fp4_scales), fp4_scale_stride, amax_out,
+                                  static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "append launch");
+  return MLA_OK;
+}
+
 int mla_plan(const int32_t* kv_indptr, int batch, int q_seq_len, int num_heads, int kv_mode, void* workspace,
              int64_t workspace_bytes, void* stream) {
   int rc = check_shape(batch, num_heads, kv_mode);

@@ -201,11 +201,12 @@ __global__ __launch_bounds__(256, 1) void decode_h16_kernel(const DecodeParams p
       if (lane == 0) xu[w] = m;
       lds_barrier();
       qs = fp8_scale_from_amax(max(max(xu[0], xu[1]), max(xu[2], xu[3])));
+      const Fp8Quant qq = make_fp8_quant(qs);
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
         const int i = tid + 256 * j;
         if (i < NV) {
-          *reinterpret_cast<uint2*>(qst + 8 * i) = quant8_fp8(xv[j], qs);
+          *reinterpret_cast<uint2*>(qst + 8 * i) = quant8_fp8(xv[j], qq);
         }
       }
       lds_barrier();

@@ -102,13 +102,32 @@ __device__ __forceinline__ float fp8_scale_from_amax(uint32_t amax_bits) {
   return bf16_bits_to_f32(f32_to_bf16_bits(a / 448.0f));
 }
 
-// clamp(bf16(x / s), -448, 448) of reference.py:79-80, exact in f32
-__device__ __forceinline__ float quant_y(uint32_t h, float s) {
-  const float y = bf16_bits_to_f32(f32_to_bf16_bits(bf16_bits_to_f32(h) / s));
+// Per-tensor fp8 quantizer state: the scale and, when it is safe, its
+// reciprocal (r = 0 selects the plain division for every element).
+struct Fp8Quant {
+  float s;
+  float r;
+};
+__device__ __forceinline__ Fp8Quant make_fp8_quant(float s) {
+  const float a = fabsf(s);
+  const bool ok = a >= 0x1p-125f && a <= 0x1p125f;  // 1/s stays a normal f32
+  return Fp8Quant{s, ok ? 1.0f / s : 0.0f};
+}
+
+// clamp(bf16(x / s), -448, 448) of reference.py:79-80, exact.  x * r (r the
+// correctly rounded 1/s) is within 3 f32 ulps of x / s's correctly rounded
+// quotient (two roundings of at most half an ulp each on top of the
+// reciprocal's), so both round to the same bf16 unless x * r lies within 3
+// ulps of a bf16 tie (low half 0x8000); only there is the division computed.
+__device__ __forceinline__ float quant_y(uint32_t h, Fp8Quant q) {
+  const float x = bf16_bits_to_f32(h);
+  float d = x * q.r;
+  if (q.r == 0.0f || (__float_as_uint(d) & 0xFFFFu) - 0x7FFDu <= 6u) d = x / q.s;
+  const float y = bf16_bits_to_f32(f32_to_bf16_bits(d));
   return fminf(fmaxf(y, -448.0f), 448.0f);
 }
 // y = e4m3fn(clamp(bf16(x / s), -448, 448)), reference.py:79-80
-__device__ __forceinline__ uint32_t quant_one(uint32_t h, float s) { return f32_to_e4m3fn(quant_y(h, s)); }
+__device__ __forceinline__ uint32_t quant_one(uint32_t h, Fp8Quant q) { return f32_to_e4m3fn(quant_y(h, q)); }
 
 // ---- wave helpers ------------------------------------------------------------
 __device__ __forceinline__ float shfl_xor_f(float v, int mask) {
@@ -161,11 +180,11 @@ __device__ __forceinline__ uint32_t pack4_fp8(float a, float b, float c, float d
 // eight bf16 (one uint4) -> eight e4m3fn codes of the per-tensor quantizer; the
 // hardware convert rounds to nearest even like the reference cast, and after
 // the clamp to +-448 no input can overflow it
-__device__ __forceinline__ uint2 quant8_fp8(uint4 v, float s) {
-  return make_uint2(pack4_fp8(quant_y(v.x & 0xFFFFu, s), quant_y(v.x >> 16, s), quant_y(v.y & 0xFFFFu, s),
-                              quant_y(v.y >> 16, s)),
-                    pack4_fp8(quant_y(v.z & 0xFFFFu, s), quant_y(v.z >> 16, s), quant_y(v.w & 0xFFFFu, s),
-                              quant_y(v.w >> 16, s)));
+__device__ __forceinline__ uint2 quant8_fp8(uint4 v, Fp8Quant q) {
+  return make_uint2(pack4_fp8(quant_y(v.x & 0xFFFFu, q), quant_y(v.x >> 16, q), quant_y(v.y & 0xFFFFu, q),
+                              quant_y(v.y >> 16, q)),
+                    pack4_fp8(quant_y(v.z & 0xFFFFu, q), quant_y(v.z >> 16, q), quant_y(v.w & 0xFFFFu, q),
+                              quant_y(v.w >> 16, q)));
 }
 
 // ---- LDS DMA (global_load_lds) and explicit waits --------------------------

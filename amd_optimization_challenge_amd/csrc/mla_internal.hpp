@@ -10,6 +10,8 @@ namespace mla {
 
 // Blocks used by the amax pass (also the number of partial maxima written).
 constexpr int kAmaxMaxBlocks = 1024;
+// Largest token count of one mla_append_kv call (72 lanes per token stay below 2^31).
+constexpr int64_t kAppendMaxTokens = (1LL << 31) / (kQKDim / 8);
 // Byte size of the quantizer scratch area at the front of every workspace.
 constexpr int64_t kQuantScratchBytes = 8192;
 
@@ -39,6 +41,10 @@ hipError_t launch_pack_mxfp4(const uint16_t* x, int64_t rows, int cols, int64_t 
                              int64_t scale_stride, hipStream_t stream);
 hipError_t launch_plan(const int32_t* kv_indptr, int batch, int qlen, int target_items, int max_items,
                        int32_t* plan, hipStream_t stream);
+hipError_t launch_append_kv(const uint16_t* x, int64_t n, int64_t x_stride, const int32_t* slots,
+                            uint8_t* fp8_cache, int64_t fp8_stride, const float* fp8_scale,
+                            uint8_t* fp4_cache, int64_t fp4_stride, uint8_t* fp4_scales,
+                            int64_t fp4_scale_stride, uint32_t* amax_out, hipStream_t stream);
 
 // decode.hip
 hipError_t launch_decode(const DecodeParams& p, int kv_mode, int grid, hipStream_t stream);

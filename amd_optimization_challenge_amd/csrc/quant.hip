@@ -9,6 +9,7 @@
 //
 // MXFP4 (reference.py:88-113 -> mxfp4-mm/submission_v18_custom_fused.py:26-108):
 // one thread per 32-element block, 64 B in (4 x 16-byte loads), 16 B + 1 B out.
+// KV-cache append: one lane per 8 elements into both caches at given rows.
 #include "mla_internal.hpp"
 
 namespace mla {
@@ -83,7 +84,7 @@ __global__ __launch_bounds__(256) void quant_fp8_kernel(const uint16_t* __restri
     if (blockIdx.x == 0) out_scale[0] = s_scale;
   }
   __syncthreads();
-  const float s = s_scale;
+  const Fp8Quant s = make_fp8_quant(s_scale);
   const int64_t nvec = n >> 3;
   const uint4* xv = reinterpret_cast<const uint4*>(x);
   uint2* ov = reinterpret_cast<uint2*>(out);
@@ -96,25 +97,69 @@ __global__ __launch_bounds__(256) void quant_fp8_kernel(const uint16_t* __restri
 }
 
 // ---------------------------------------------------------------------------
-// MXFP4 pack: e8m0 scale rule and e2m1 rounding of
-// mxfp4-mm/submission_v18_custom_fused.py:50-106 in integer form
+// MXFP4 pack: e8m0 scale rule of mxfp4-mm/submission_v18_custom_fused.py:50-58
+// in integer form; e2m1 rounding (:60-98) by the hardware conversion
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ uint32_t e2m1_encode(float q) {
-  uint32_t u = __float_as_uint(q);
-  uint32_t s = u & 0x80000000u;
-  u ^= s;
-  float a = __uint_as_float(u);
-  uint32_t code;
-  if (a >= 6.0f) {
-    code = 7u;
-  } else if (a < 1.0f) {
-    // add 2^22 so the f32 add rounds |q| to a multiple of 0.5 (ties to even)
-    code = __float_as_uint(a + 4194304.0f) - (149u << 23);
-  } else {
-    uint32_t odd = (u >> 22) & 1u;
-    code = ((u + 0xC1200000u - 1u + odd) >> 22) & 0xFFu;  // (1-127)<<23 + 2^21 - 1 (mod 2^32)
+// e8m0 exponent of a 32-element block from the f32 bits of its |x| max: round
+// the max up at bit 21, take the f32 exponent, subtract 2 (emax of e2m1),
+// clamp to [-127, 127].
+__device__ __forceinline__ int mx_exponent(uint32_t amax_f32_bits) {
+  const uint32_t rnd = (amax_f32_bits + 0x200000u) & 0xFF800000u;
+  const int ef = (int)(rnd >> 23);
+  if (ef == 0) return -127;   // log2(0) = -inf, clamped
+  if (ef == 255) return 127;  // +inf after round-up, clamped
+  return min(max(ef - 127 - 2, -127), 127);
+}
+
+// 2^-e as an f32 (2^-127 is the one subnormal case)
+__device__ __forceinline__ float mx_qscale(int e) {
+  return (e == 127) ? __uint_as_float(0x00400000u) : __uint_as_float((uint32_t)(127 - e) << 23);
+}
+
+// Four words of bf16 pairs -> four bytes of e2m1 pairs (low nibble = low
+// half) after scaling by qs = 2^-e (exact).  The hardware conversion rounds
+// to nearest, ties to the even code, and saturates at 6 -- the rule of
+// the reference's bit-trick encoder (mxfp4-mm/submission_v18_custom_fused.py:
+// 66-98) -- which a device selftest pins on every value it can receive.
+__device__ __forceinline__ uint32_t mx_encode_word4(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3, float qs) {
+  uint32_t r = 0;
+  r = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(r, bf16_bits_to_f32(w0 & 0xFFFFu) * qs,
+                                               bf16_bits_to_f32(w0 >> 16) * qs, 1.0f, 0);
+  r = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(r, bf16_bits_to_f32(w1 & 0xFFFFu) * qs,
+                                               bf16_bits_to_f32(w1 >> 16) * qs, 1.0f, 1);
+  r = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(r, bf16_bits_to_f32(w2 & 0xFFFFu) * qs,
+                                               bf16_bits_to_f32(w2 >> 16) * qs, 1.0f, 2);
+  r = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(r, bf16_bits_to_f32(w3 & 0xFFFFu) * qs,
+                                               bf16_bits_to_f32(w3 >> 16) * qs, 1.0f, 3);
+  return r;
+}
+
+// One 32-element block: 16 words of bf16 pairs in, 16 bytes of e2m1 pairs and
+// the e8m0 byte out.
+__device__ __forceinline__ uint4 mx_block_encode(const uint32_t (&w)[16], uint32_t& e8) {
+  uint32_t amax = 0;  // f32 bits of the block |x| max
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    amax = max(amax, (w[k] & 0x7FFFu) << 16);
+    amax = max(amax, (w[k] >> 16 & 0x7FFFu) << 16);
   }
-  return code | (s >> 28);
+  const int e = mx_exponent(amax);
+  const float qs = mx_qscale(e);
+  e8 = (uint32_t)(e + 127);
+  return make_uint4(mx_encode_word4(w[0], w[1], w[2], w[3], qs), mx_encode_word4(w[4], w[5], w[6], w[7], qs),
+                    mx_encode_word4(w[8], w[9], w[10], w[11], qs), mx_encode_word4(w[12], w[13], w[14], w[15], qs));
+}
+
+__device__ __forceinline__ void load_block64(const uint8_t* p, uint32_t (&w)[16]) {
+  const uint4* src = reinterpret_cast<const uint4*>(p);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    uint4 v = src[k];
+    w[4 * k + 0] = v.x;
+    w[4 * k + 1] = v.y;
+    w[4 * k + 2] = v.z;
+    w[4 * k + 3] = v.w;
+  }
 }
 
 __global__ __launch_bounds__(256) void pack_mxfp4_kernel(const uint8_t* __restrict__ x, int64_t rows,
@@ -127,40 +172,72 @@ __global__ __launch_bounds__(256) void pack_mxfp4_kernel(const uint8_t* __restri
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
     const int64_t r = i / blocks_per_row;
     const int j = (int)(i - r * blocks_per_row);
-    const uint4* src = reinterpret_cast<const uint4*>(x + r * x_stride + (int64_t)j * 64);
     uint32_t w[16];
+    load_block64(x + r * x_stride + (int64_t)j * 64, w);
+    uint32_t e8;
+    *reinterpret_cast<uint4*>(packed + r * packed_stride + (int64_t)j * 16) = mx_block_encode(w, e8);
+    scales[r * scale_stride + j] = (uint8_t)e8;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// KV-cache append: token i (576 bf16) goes to cache row slots[i] of the fp8
+// cache (quantized with the cache's existing per-tensor scale, the bytes the
+// whole-buffer quantizer gives for that scale) and/or of the mxfp4 cache (its
+// per-32 blocks need no global state, so an appended row equals the row of a
+// whole-buffer pack).  slot < 0 skips the token.  amax_out (optional) is
+// max-ed with the bf16 bits of max|x| over the written tokens.
+//
+// One lane per 8 elements (72 lanes per token): 16 B loads and 8 B / 4 B
+// stores are contiguous across lanes, and a 32-element block is 4 aligned
+// lanes that exchange their |x| max by two shuffles.  Lane groups of 4 never
+// straddle a token (72 = 4 * 18) or a wave (64 = 4 * 16), and a whole token is
+// skipped or written, so the 4 lanes of a block are active together.
+// ---------------------------------------------------------------------------
+constexpr int kLanesPerToken = kQKDim / 8;  // 72
+
+__global__ __launch_bounds__(256) void append_kv_kernel(
+    const uint8_t* __restrict__ x, int n, int64_t x_stride, const int32_t* __restrict__ slots,
+    uint8_t* __restrict__ fp8_cache, int64_t fp8_stride, const float* __restrict__ fp8_scale,
+    uint8_t* __restrict__ fp4_cache, int64_t fp4_stride, uint8_t* __restrict__ fp4_scales,
+    int64_t fp4_scale_stride, uint32_t* __restrict__ amax_out) {
+  const uint32_t total = (uint32_t)n * kLanesPerToken;
+  const Fp8Quant s = make_fp8_quant(fp8_cache != nullptr ? fp8_scale[0] : 1.0f);
+  uint32_t amax = 0;  // bf16 |x| bits over this lane's written chunks
+  for (uint32_t u = blockIdx.x * 256u + threadIdx.x; u < total; u += gridDim.x * 256u) {
+    const uint32_t t = u / kLanesPerToken;
+    const uint32_t p = u - t * kLanesPerToken;
+    const int64_t slot = slots != nullptr ? (int64_t)slots[t] : (int64_t)t;
+    if (slot < 0) continue;
+    const uint4 v = ldg16_nt(x + (int64_t)t * x_stride + p * 16);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    uint32_t m = 0;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      uint4 v = src[k];
-      w[4 * k + 0] = v.x;
-      w[4 * k + 1] = v.y;
-      w[4 * k + 2] = v.z;
-      w[4 * k + 3] = v.w;
+    for (int k = 0; k < 4; ++k) m = max(m, max(w[k] & 0x7FFFu, (w[k] >> 16) & 0x7FFFu));
+    amax = max(amax, m);
+    if (fp8_cache != nullptr)
+      *reinterpret_cast<uint2*>(fp8_cache + slot * fp8_stride + p * 8) = quant8_fp8(v, s);
+    if (fp4_cache != nullptr) {
+      m = max(m, (uint32_t)__shfl_xor((int)m, 1, 64));
+      m = max(m, (uint32_t)__shfl_xor((int)m, 2, 64));
+      const int e = mx_exponent(m << 16);
+      const float qs = mx_qscale(e);
+      *reinterpret_cast<uint32_t*>(fp4_cache + slot * fp4_stride + p * 4) = mx_encode_word4(w[0], w[1], w[2], w[3], qs);
+      if ((p & 3u) == 0) fp4_scales[slot * fp4_scale_stride + (p >> 2)] = (uint8_t)(e + 127);
     }
-    uint32_t amax = 0;  // f32 bits of the block |x| max
+  }
+  if (amax_out != nullptr) {
+    // one atomic per block at most, and only when it raises the stored max:
+    // atomics on one address serialize, so per-wave atomics would dominate
+    __shared__ uint32_t red[4];
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      amax = max(amax, (w[k] & 0x7FFFu) << 16);
-      amax = max(amax, (w[k] >> 16 & 0x7FFFu) << 16);
+    for (int off = 32; off > 0; off >>= 1) amax = max(amax, (uint32_t)__shfl_xor((int)amax, off, 64));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const uint32_t m = max(max(red[0], red[1]), max(red[2], red[3]));
+      if (m > __atomic_load_n(amax_out, __ATOMIC_RELAXED)) atomicMax(amax_out, m);
     }
-    const uint32_t rnd = (amax + 0x200000u) & 0xFF800000u;
-    const int ef = (int)(rnd >> 23);
-    int e;
-    if (ef == 0) e = -127;           // log2(0) = -inf, clamped
-    else if (ef == 255) e = 127;     // +inf after round-up, clamped
-    else e = min(max(ef - 127 - 2, -127), 127);
-    // 2^-e as an f32 (2^-127 is the one subnormal case)
-    const float qs = (e == 127) ? __uint_as_float(0x00400000u) : __uint_as_float((uint32_t)(127 - e) << 23);
-    uint32_t outw[4] = {0, 0, 0, 0};
-#pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      uint32_t c0 = e2m1_encode(bf16_bits_to_f32(w[k] & 0xFFFFu) * qs);
-      uint32_t c1 = e2m1_encode(bf16_bits_to_f32(w[k] >> 16) * qs);
-      outw[k >> 2] |= (c0 | (c1 << 4)) << (8 * (k & 3));
-    }
-    *reinterpret_cast<uint4*>(packed + r * packed_stride + (int64_t)j * 16) =
-        make_uint4(outw[0], outw[1], outw[2], outw[3]);
-    scales[r * scale_stride + j] = (uint8_t)(e + 127);
   }
 }
 
@@ -365,6 +442,19 @@ hipError_t launch_pack_mxfp4(const uint16_t* x, int64_t rows, int cols, int64_t 
   hipLaunchKernelGGL(pack_mxfp4_kernel, dim3((int)g), dim3(256), 0, stream,
                      reinterpret_cast<const uint8_t*>(x), rows, bpr, x_stride, packed,
                      packed_stride, scales, scale_stride);
+  return hipGetLastError();
+}
+
+hipError_t launch_append_kv(const uint16_t* x, int64_t n, int64_t x_stride, const int32_t* slots,
+                            uint8_t* fp8_cache, int64_t fp8_stride, const float* fp8_scale,
+                            uint8_t* fp4_cache, int64_t fp4_stride, uint8_t* fp4_scales,
+                            int64_t fp4_scale_stride, uint32_t* amax_out, hipStream_t stream) {
+  int64_t g = (n * kLanesPerToken + 255) / 256;
+  if (g < 1) g = 1;
+  if (g > 2048) g = 2048;  // 8 blocks per CU; larger appends loop
+  hipLaunchKernelGGL(append_kv_kernel, dim3((int)g), dim3(256), 0, stream,
+                     reinterpret_cast<const uint8_t*>(x), (int)n, x_stride, slots, fp8_cache, fp8_stride,
+                     fp8_scale, fp4_cache, fp4_stride, fp4_scales, fp4_scale_stride, amax_out);
   return hipGetLastError();
 }
 

@@ -133,6 +133,24 @@ __global__ void selftest_kernel(int which, const uint8_t* __restrict__ in, uint8
   } else if (which == 9) {  // software f32 -> e4m3fn: 256 floats -> 256 bytes
     const float* x = reinterpret_cast<const float*>(in);
     for (int i = 0; i < 4; ++i) out[4 * l + i] = (uint8_t)f32_to_e4m3fn(x[4 * l + i]);
+  } else if (which == 20) {  // hardware f32 pair -> e2m1 byte: 4096 floats + f32 scale -> 4096 bytes
+    // pair i goes to byte i % 4 of a word that starts as 0xA5A5A5A5; out[i] =
+    // that byte, out[2048 + i] = 1 if the other three bytes were kept
+    const float* x = reinterpret_cast<const float*>(in);
+    const float sc = x[4096];
+    for (int i = l; i < 2048; i += 64) {
+      const uint32_t old = 0xA5A5A5A5u;
+      uint32_t r;
+      switch (i & 3) {
+        case 0: r = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(old, x[2 * i], x[2 * i + 1], sc, 0); break;
+        case 1: r = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(old, x[2 * i], x[2 * i + 1], sc, 1); break;
+        case 2: r = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(old, x[2 * i], x[2 * i + 1], sc, 2); break;
+        default: r = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(old, x[2 * i], x[2 * i + 1], sc, 3); break;
+      }
+      const int sh = 8 * (i & 3);
+      out[i] = (uint8_t)((r >> sh) & 0xFFu);
+      out[2048 + i] = (uint8_t)(((r | (0xFFu << sh)) == (old | (0xFFu << sh))) ? 1 : 0);
+    }
   } else if (which == 10) {  // hardware e4m3fn -> f32: 64 words -> 256 floats
     const int word = reinterpret_cast<const int*>(in)[l];
     const v2f lo = __builtin_amdgcn_cvt_pk_f32_fp8(word, false);
@@ -235,7 +253,8 @@ hipError_t launch_selftest(int which, const void* in, void* out, hipStream_t str
                        static_cast<float*>(out));
     return hipGetLastError();
   }
-  if (which < 0 || (which > 10 && which != 15 && which != 16 && which != 19)) return hipErrorInvalidValue;
+  if (which < 0 || (which > 10 && which != 15 && which != 16 && which != 19 && which != 20))
+    return hipErrorInvalidValue;
   hipLaunchKernelGGL(selftest_kernel, dim3(1), dim3(64), 0, stream, which,
                      static_cast<const uint8_t*>(in), static_cast<uint8_t*>(out));
   return hipGetLastError();

@@ -130,6 +130,54 @@ def pack_mxfp4(x: torch.Tensor, scale_cols: int | None = None):
     return packed.reshape(*x.shape[:-1], cols // 2), scales
 
 
+def append_kv(x: torch.Tensor, slots: torch.Tensor | None, fp8=None, mxfp4=None,
+              amax: torch.Tensor | None = None) -> None:
+    """Write bf16 tokens ``x`` [n, 576] (or [n, 1, 576]) into cache rows ``slots``.
+
+    ``fp8`` = (cache [rows, 1, 576] e4m3fn, scale [1] f32): quantized with the
+    cache's existing scale, the bytes quantize_fp8
+    (competitor_submissions/mi355x_reference/reference.py:65-80) gives for the
+    whole buffer at that scale.  ``mxfp4`` = (cache [rows, 1, 288] fp4x2,
+    e8m0 [rows, >= 18]): the row's dynamic_mxfp4_quant bytes (reference.py:88-113).
+    ``slots`` int32 [n] (None = rows 0..n-1, negative = skip).  ``amax``
+    (int32 [1], optional) is max-ed with the bf16 bits of max|x|.  The slots
+    are trusted to be in range and distinct, like the decode's kv_indices.
+    """
+    if fp8 is None and mxfp4 is None:
+        raise ValueError("append_kv needs an fp8 and/or an mxfp4 cache")
+    _require_cuda(x, slots, amax)
+    if x.dtype != torch.bfloat16 or x.shape[-1] != QK_DIM:
+        raise ValueError("x must be bfloat16 [..., 576]")
+    x2 = x.reshape(-1, QK_DIM)
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    n = x2.shape[0]
+    if slots is not None:
+        if slots.dtype != torch.int32 or slots.numel() != n:
+            raise ValueError("slots must be int32 with one entry per token")
+        slots = slots.contiguous()
+    if amax is not None and (amax.dtype != torch.int32 or amax.numel() < 1):
+        raise ValueError("amax must be an int32 tensor of >= 1 element")
+    f8 = f8_scale = f4 = f4_scales = None
+    f8_stride = f4_stride = f4_scale_stride = 0
+    if fp8 is not None:
+        cache, f8_scale = fp8
+        f8 = as_bytes(cache).reshape(cache.shape[0], -1)
+        f8_stride = f8.stride(0)
+        _require_cuda(f8, f8_scale)
+    if mxfp4 is not None:
+        cache, sc = mxfp4
+        f4 = as_bytes(cache).reshape(cache.shape[0], -1)
+        f4_scales = as_bytes(sc)
+        f4_stride, f4_scale_stride = f4.stride(0), f4_scales.stride(0)
+        _require_cuda(f4, f4_scales)
+    with torch.cuda.device(x.device):
+        _lib.check(_lib.load().mla_append_kv(_ptr(x2), n, x2.stride(0) * 2, _ptr(slots), _ptr(f8), f8_stride,
+                                             _ptr(f8_scale), _ptr(f4), f4_stride, _ptr(f4_scales),
+                                             f4_scale_stride, _ptr(amax), _stream()),
+                   "mla_append_kv")
+
+
 # ---------------------------------------------------------------------------
 # decode pipeline stages
 # ---------------------------------------------------------------------------

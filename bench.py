@@ -216,6 +216,38 @@ def profile_decode(cids, reps):
         torch.cuda.empty_cache()
 
 
+def bench_append(n_tokens, steps, warmup):
+    """KV-cache append (mla_append_kv) of n_tokens permuted rows into both
+    caches: mean device time per call and the HBM rate of its algorithmic
+    bytes (1152 B bf16 in + 576 fp8 + 288 e2m1 + 18 e8m0 + 4 slot per token)."""
+    import torch
+
+    from amd_optimization_challenge_amd import ops
+
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn((n_tokens, 576), generator=g, dtype=torch.bfloat16).cuda()
+    slots = torch.randperm(n_tokens, generator=g).to(torch.int32).cuda()
+    f8 = torch.empty((n_tokens, 1, 576), dtype=torch.float8_e4m3fn, device="cuda")
+    f4 = torch.empty((n_tokens, 1, 288), dtype=torch.uint8, device="cuda")
+    sc = torch.empty((n_tokens, 18), dtype=torch.uint8, device="cuda")
+    _, scale = ops.quant_fp8_per_tensor(x)
+    amax = torch.zeros(1, dtype=torch.int32, device="cuda")
+    for _ in range(warmup):
+        ops.append_kv(x, slots, fp8=(f8, scale), mxfp4=(f4, sc), amax=amax)
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    ev[0].record()
+    for _ in range(steps):
+        ops.append_kv(x, slots, fp8=(f8, scale), mxfp4=(f4, sc), amax=amax)
+    ev[1].record()
+    torch.cuda.synchronize()
+    us = ev[0].elapsed_time(ev[1]) * 1e3 / steps
+    nbytes = n_tokens * (1152 + 576 + 288 + 18 + 4)
+    gbs = nbytes / (us * 1e-6) / 1e9
+    return {"kernel": "append_kv (fp8 + mxfp4 rows)", "tokens": n_tokens, "steps": steps, "us_per_call": round(us, 3),
+            "bytes_per_launch": nbytes, "achieved_GBs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -225,6 +257,8 @@ def main(argv=None):
     ap.add_argument("--only-headline", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-budget-s", type=float, default=10.0)
+    ap.add_argument("--append-tokens", type=int, default=0,
+                    help="time the KV-cache append writer at this many tokens instead (own JSON line)")
     ap.add_argument("--profile-decode", action="store_true",
                     help="decode-only launches for counter collection (no JSON line)")
     args = ap.parse_args(argv)
@@ -237,6 +271,9 @@ def main(argv=None):
     from amd_optimization_challenge_amd import _lib, inputs
 
     _lib.load()
+    if args.append_tokens > 0:
+        print(json.dumps(bench_append(args.append_tokens, args.steps, args.warmup)), flush=True)
+        return 0
     if args.profile_decode:
         profile_decode([args.config] if args.only_headline else sorted(inputs.CONFIGS), max(1, args.steps))
         return 0

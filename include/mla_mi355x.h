@@ -89,6 +89,29 @@ int mla_pack_mxfp4(const void* x_bf16, int64_t rows, int cols, int64_t x_row_str
                    int64_t scale_row_stride, void* stream);
 
 /*
+ * KV-cache append: writes n new tokens (bf16 [n, 576], row stride in bytes)
+ * into cache rows slots[i] (page size 1; slots == NULL means row i; a negative
+ * slot skips its token; slots must be distinct; n <= 29826161 per call).
+ * Either cache may be NULL, not both.
+ *   fp8 cache   : e4m3fn(clamp(bf16(x / fp8_scale[0]), +-448)) with the
+ *                 cache's existing per-tensor scale -- the bytes quantize_fp8
+ *                 gives for the whole buffer when its scale is fp8_scale[0]
+ *   mxfp4 cache : e2m1 pairs + e8m0 per 32 elements, bit-exact to
+ *                 dynamic_mxfp4_quant of the row; scale stride >= 18 (padded
+ *                 columns are not written)
+ * amax_out (optional, device u32) is max-ed with the bf16 bits of max|x| over
+ * the written tokens; tokens above 448 * fp8_scale saturate in the fp8 cache,
+ * which the caller detects by comparing it with the scale.  The reference
+ * builds its caches whole (competitor_submissions/mi355x_reference/
+ * reference.py:318-321, layout competitor_submissions/mi355x_reference/
+ * README.md:57-81); this is the incremental writer of the same bytes.
+ */
+int mla_append_kv(const void* x_bf16, int64_t n, int64_t x_row_stride, const int32_t* slots,
+                  void* fp8_cache, int64_t fp8_row_stride, const float* fp8_scale, void* fp4_cache,
+                  int64_t fp4_row_stride, void* fp4_scales, int64_t fp4_scale_stride, uint32_t* amax_out,
+                  void* stream);
+
+/*
  * Split-KV work partition, computed on the device from kv_indptr (no host
  * sync).  Replaces get_mla_metadata_v1
  * (competitor_submissions/mi355x_reference/reference.py:161-209) and the

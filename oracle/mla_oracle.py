@@ -5,7 +5,9 @@ TEST INFRASTRUCTURE ONLY.  Only ``tests/``, ``__graft_entry__.smoke()`` and the
 checker (or as the timed CPU baseline).  The product path never routes through
 it: ``amd_optimization_challenge_amd`` raises if its HIP library is missing.
 
-What it restates (all citations relative to the reference checkout):
+What it restates (all citations relative to the reference checkout; ``TASK/``
+stands for competitor_submissions/mi355x_reference/, the in-tree copy of the
+task files):
 
 * ``quantize_fp8_per_tensor``  -- TASK/reference.py:65-80 (``quantize_fp8``),
   with torch's bf16 arithmetic made explicit: |x| max in bf16, clamp(min=1e-12)
@@ -16,6 +18,9 @@ What it restates (all citations relative to the reference checkout):
   mxfp4-mm/submission_v18_custom_fused.py:26-108 (``_mxfp4_quant_op``).
   AITER itself is not vendored (un-pinned HEAD clone, setup.sh:52-61), so the
   restatement there is the anchor.
+* ``quantize_fp8_with_scale`` / ``append_kv`` -- the element step of
+  TASK/reference.py:79-80 at a given scale, and the row-scatter cache writer
+  built from it and ``pack_mxfp4`` (the incremental form of reference.py:318-321).
 * ``dequant_fp8`` / ``dequant_mxfp4`` -- TASK/reference.py:73-74 and
   TASK/reference.py:116-154; e2m1 table from mixed-mla/triton_mla_mxfp4.py:21-31,
   e8m0 = 2^(e-127) from mixed-mla/triton_mla_mxfp4.py:59.
@@ -34,6 +39,9 @@ Parity pins (see tests/test_oracle_*.py):
   mxfp4 pack  -- exhaustive element encoding against the reference's bit-trick
                  formula (restated in the test), scale-rule known answers,
                  round trip.
+  append      -- identity slots with the whole-buffer scale reproduce
+                 quantize_fp8_per_tensor / pack_mxfp4; permuted slots give a
+                 row permutation; saturation and exact-grid closed forms.
   attention   -- float64 brute force on tiny shapes, closed forms (kv_len=1,
                  identical keys), permutation/split invariance.
 """
@@ -165,11 +173,39 @@ def quantize_fp8_per_tensor(x_bits: np.ndarray) -> tuple[np.ndarray, float]:
     mag = (bits & 0x7FFF).astype(np.uint32)
     amax_bits = int(mag.max()) if mag.size else 0
     s_bits, scale = fp8_scale_from_amax_bits(amax_bits)
-    xf = bf16_to_f32(bits)
-    y_bits = f32_to_bf16(xf / np.float32(scale))
-    y = bf16_to_f32(y_bits)
-    y = np.clip(y, -FP8_MAX, FP8_MAX)
-    return f32_to_e4m3fn(y), np.float32(scale)
+    return quantize_fp8_with_scale(bits, scale), np.float32(scale)
+
+
+def quantize_fp8_with_scale(x_bits: np.ndarray, scale: float) -> np.ndarray:
+    """The element step of TASK/reference.py:79-80 for a given f32 scale:
+    e4m3fn_rne(clamp(bf16(x / scale), -448, 448)).  With the whole buffer's
+    scale this is what ``quantize_fp8`` writes for any subset of its rows."""
+    xf = bf16_to_f32(np.asarray(x_bits, dtype=np.uint16))
+    y = bf16_to_f32(f32_to_bf16(xf / np.float32(scale)))
+    return f32_to_e4m3fn(np.clip(y, -FP8_MAX, FP8_MAX))
+
+
+def append_kv(x_bits, slots, fp8_cache=None, fp8_scale=None, fp4_cache=None, fp4_scales=None):
+    """Write tokens x_bits [n, 576] (bf16 bits) into cache rows ``slots`` in place.
+
+    The incremental form of the cache build at TASK/reference.py:318-321:
+    fp8 rows with a fixed per-tensor scale (``quantize_fp8_with_scale``), mxfp4
+    rows with their own block scales (``pack_mxfp4`` of the row; scale columns
+    beyond 18 untouched).  ``slots`` None = rows 0..n-1; a negative slot skips.
+    Returns the bf16 bits of max|x| over the written tokens (0 if none).
+    """
+    x = np.asarray(x_bits, dtype=np.uint16).reshape(-1, QK_DIM)
+    n = x.shape[0]
+    idx = np.arange(n) if slots is None else np.asarray(slots, dtype=np.int64).reshape(n)
+    keep = idx >= 0
+    xs, rows = x[keep], idx[keep]
+    if fp8_cache is not None:
+        fp8_cache.reshape(fp8_cache.shape[0], -1)[rows, :QK_DIM] = quantize_fp8_with_scale(xs, fp8_scale)
+    if fp4_cache is not None:
+        packed, e8 = pack_mxfp4(xs)
+        fp4_cache.reshape(fp4_cache.shape[0], -1)[rows, :QK_DIM // 2] = packed
+        fp4_scales[rows, :QK_DIM // MX_BLOCK] = e8
+    return int((xs & 0x7FFF).max()) if xs.size else 0
 
 
 def dequant_fp8(codes: np.ndarray, scale: float) -> np.ndarray:

@@ -40,6 +40,19 @@ def test_argument_errors_without_device():
     assert lib.mla_pack_mxfp4(None, 4, 33, 66, None, 16, None, 2, None) == _lib.MLA_ERR_INVALID_ARGUMENT
     assert lib.mla_quant_fp8_per_tensor(None, 0, None, None, None, 0, None) == _lib.MLA_ERR_INVALID_ARGUMENT
     assert lib.mla_selftest(0, None, None, None) == _lib.MLA_ERR_INVALID_ARGUMENT
+    # append: no cache, negative n, fp8 cache without its scale, short scale stride
+    assert lib.mla_append_kv(None, 4, 1152, None, None, 0, None, None, 0, None, 0, None,
+                             None) == _lib.MLA_ERR_INVALID_ARGUMENT
+    assert lib.mla_append_kv(None, -1, 1152, None, 16, 576, 16, None, 0, None, 0, None,
+                             None) == _lib.MLA_ERR_INVALID_ARGUMENT
+    assert lib.mla_append_kv(16, 4, 1152, None, 16, 576, None, None, 0, None, 0, None,
+                             None) == _lib.MLA_ERR_INVALID_ARGUMENT
+    assert lib.mla_append_kv(16, 4, 1152, None, None, 0, None, 16, 288, 16, 17, None,
+                             None) == _lib.MLA_ERR_INVALID_ARGUMENT
+    assert b"18" in lib.mla_last_error()
+    assert lib.mla_append_kv(16, 29826162, 1152, None, 16, 576, 16, None, 0, None, 0, None,
+                             None) == _lib.MLA_ERR_INVALID_ARGUMENT
+    assert lib.mla_append_kv(None, 0, 0, None, 16, 0, None, None, 0, None, 0, None, None) == _lib.MLA_OK
     with pytest.raises(_lib.MlaLibraryError):
         _lib.check(lib.mla_workspace_bytes(4, 24, 0, ctypes.byref(n)), "mla_workspace_bytes")
     # q_seq_len must divide the query rows (checked before any device call)

@@ -11,7 +11,8 @@ pytestmark = pytest.mark.gpu
 
 
 IN_BYTES = {0: 4096, 1: 4096, 2: 3136, 3: 3136, 4: 1024, 5: 2048, 6: 1024, 7: 512, 8: 1024, 9: 1024,
-            10: 256, 11: 0, 12: 0, 13: 1024, 14: 1024, 15: 4160, 16: 4160, 17: 1024, 18: 1024, 19: 4160}
+            10: 256, 11: 0, 12: 0, 13: 1024, 14: 1024, 15: 4160, 16: 4160, 17: 1024, 18: 1024, 19: 4160,
+            20: 16388}
 
 
 def run(which, inp: np.ndarray, out_bytes: int) -> np.ndarray:
@@ -238,3 +239,57 @@ def test_lds_dma_subdword_placement(cuda, which, width):
     exp[:, :width] = src[: 64 * width].reshape(64, width)
     assert np.array_equal(got[:256].reshape(64, 4), exp)
     assert np.all(got[256:] == 0xEE)
+
+
+def _e2m1_hw(x: np.ndarray, scale: float) -> np.ndarray:
+    """Hardware f32 -> e2m1 conversion (selftest 20), 4096 values per call."""
+    codes = []
+    for lo in range(0, len(x), 4096):
+        chunk = np.zeros(4096, np.float32)
+        part = x[lo:lo + 4096]
+        chunk[:len(part)] = part
+        out = run(20, np.concatenate([chunk, np.array([scale], np.float32)]), 4096)
+        got, kept = out[:2048], out[2048:]
+        assert kept.all(), "byte select disturbed the other bytes"
+        pairs = np.stack([got & 0xF, got >> 4], axis=1).reshape(-1)
+        codes.append(pairs[:len(part)])
+    return np.concatenate(codes).astype(np.uint8)
+
+
+def test_hw_e2m1_convert_exhaustive(cuda):
+    """v_cvt_scalef32_pk_fp4_f32 with scale 1 against the oracle's e2m1 encoder
+    (nearest, ties to the even code, >= 6 saturates) on every non-NaN bf16
+    value: that is every value x * 2^-e the MXFP4 packer can feed it, since the
+    block scale only shifts exponents of bf16 inputs."""
+    allb = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    keep = ~(((allb & 0x7F80) == 0x7F80) & ((allb & 0x7F) != 0))  # drop NaN, keep +-inf
+    bits = allb[keep]
+    x = O.bf16_to_f32(bits)
+    got = _e2m1_hw(x, 1.0)
+    want = O.f32_to_e2m1(x)
+    bad = np.nonzero(got != want)[0]
+    assert bad.size == 0, [(hex(int(bits[i])), float(x[i]), int(got[i]), int(want[i])) for i in bad[:12]]
+
+
+def test_hw_e2m1_convert_full_mantissas_and_subnormals(cuda):
+    """Random f32 inputs with full 23-bit mantissas over [-8, 8] and random f32
+    subnormals (the packer's x * 2^-e can be subnormal when e = 127)."""
+    rng = np.random.default_rng(32)
+    a = rng.uniform(-8, 8, 40000).astype(np.float32)
+    sub = (rng.integers(1, 1 << 23, 8000).astype(np.uint32) | (rng.integers(0, 2, 8000).astype(np.uint32) << 31))
+    x = np.concatenate([a, sub.view(np.float32)])
+    got = _e2m1_hw(x, 1.0)
+    want = O.f32_to_e2m1(x)
+    bad = np.nonzero(got != want)[0]
+    assert bad.size == 0, [(float(x[i]), int(got[i]), int(want[i])) for i in bad[:12]]
+
+
+def test_hw_e2m1_convert_scale_operand(cuda):
+    """Which way the scale operand of the conversion acts (x * s or x / s)."""
+    rng = np.random.default_rng(31)
+    x = (rng.standard_normal(4096) * 3).astype(np.float32)
+    got = _e2m1_hw(x, 4.0)
+    div = O.f32_to_e2m1((x / np.float32(4.0)).astype(np.float32))
+    mul = O.f32_to_e2m1((x * np.float32(4.0)).astype(np.float32))
+    print(f"scale operand: matches x/s {np.array_equal(got, div)}, x*s {np.array_equal(got, mul)}", flush=True)
+    assert np.array_equal(got, div) or np.array_equal(got, mul)
