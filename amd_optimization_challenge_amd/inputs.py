@@ -1,10 +1,12 @@
 """Seeded synthetic inputs in the reference's ``(q, kv_data, qo_indptr, kv_indptr, config)`` layout.
 
-Restates competitor_submissions/mi355x_reference/reference.py:288-346
-(``generate_input``) with two differences that make GPU and CPU runs see the
-same bits: random numbers come from a CPU ``torch.Generator`` (the reference
-draws on the GPU), and the caches are built on the device by this package's
-own bit-exact quantizers (``ops.quant_fp8_per_tensor``/``ops.pack_mxfp4``).
+``generate_input`` is the reference's task input
+(competitor_submissions/mi355x_reference/reference.py:288-346), drawn on the
+device as the reference draws it.  ``generate``/``generate_config`` (the
+BASELINE configs and the parity tests) draw from a CPU ``torch.Generator``
+instead, so GPU and CPU runs see the same bits.  Either way the caches are
+built on the device by this package's bit-exact quantizers
+(``ops.quant_fp8_per_tensor``/``ops.pack_mxfp4``).
 
 Extensions over the reference (all optional keys, old callers unaffected):
 ``config["num_heads"]`` (16 or 128), ``config["kv_indices"]`` (page-size-1
@@ -124,13 +126,32 @@ def generate(batch, num_heads, lens, kv_mode, seed, permute=True, sm_scale=SM_SC
 
 
 def generate_input(batchsize: int, qseqlen: int, kvseqlen: int, seed: int, device="cuda"):
-    """Reference-signature generator (reference.py:288): H = 16, uniform lengths,
-    contiguous cache (kv_indices = arange), sm_scale = 1/sqrt(576), fp8 route."""
-    if qseqlen != 1:
-        raise NotImplementedError("decode only: qseqlen must be 1")
-    data = generate(batchsize, 16, ("fixed", kvseqlen), "fp8", seed, permute=False,
-                    sm_scale=1.0 / math.sqrt(QK_DIM), device=device)
-    q, kv_data, qo, kv_indptr, cfg = data
-    kv_data.update(build_kv_data(kv_data["bf16"], "mxfp4"))
-    cfg["kv_indices"] = None
-    return (q, kv_data, qo, kv_indptr, cfg)
+    """The reference's task input (competitor_submissions/mi355x_reference/
+    reference.py:288-346): H = 16, uniform lengths, contiguous cache, sm_scale =
+    1/sqrt(576), the reference's config keys only.  q and then the bf16 cache
+    are drawn from a generator on ``device`` seeded with ``seed``, in the
+    reference's order, shapes and dtypes, so a torch build that draws like the
+    reference's produces its numbers; the fp8 and mxfp4 caches come from this
+    package's bit-exact quantizers."""
+    dev = torch.device(device)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(int(seed))
+    total_q, total_kv = batchsize * qseqlen, batchsize * kvseqlen
+    q = torch.randn((total_q, 16, QK_DIM), dtype=torch.bfloat16, device=dev, generator=gen)
+    kv = torch.randn((total_kv, 1, QK_DIM), dtype=torch.bfloat16, device=dev, generator=gen)
+    kv_data = build_kv_data(kv, "mxfp4k_fp8v")
+    qo_indptr = torch.arange(0, batchsize + 1, dtype=torch.int32, device=dev) * qseqlen
+    kv_indptr = torch.arange(0, batchsize + 1, dtype=torch.int32, device=dev) * kvseqlen
+    config = {
+        "batch_size": batchsize,
+        "num_heads": 16,
+        "num_kv_heads": 1,
+        "qk_head_dim": QK_DIM,
+        "kv_lora_rank": V_DIM,
+        "qk_rope_head_dim": QK_DIM - V_DIM,
+        "v_head_dim": V_DIM,
+        "q_seq_len": qseqlen,
+        "kv_seq_len": kvseqlen,
+        "sm_scale": 1.0 / math.sqrt(QK_DIM),
+    }
+    return (q, kv_data, qo_indptr, kv_indptr, config)

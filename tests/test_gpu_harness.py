@@ -1,0 +1,48 @@
+"""The evaluation-harness loop on the device: the task's four test shapes pass
+the reference's check (and the stricter 2e-2 bound), a short leaderboard run
+produces Stats, and generate_input is deterministic."""
+import pytest
+import torch
+
+from amd_optimization_challenge_amd import custom_kernel, harness as Hn, inputs
+
+pytestmark = pytest.mark.gpu
+
+
+def test_task_tests_pass_the_reference_check(cuda):
+    lines = []
+    rc, res = Hn.run("test", Hn.task_cases("test"), log=lambda s: (lines.append(s), print(s, flush=True)))
+    assert rc == 0, "\n".join(lines)
+    assert all(m.startswith("Maximum error") for m in res.values()), res
+
+
+@pytest.mark.parametrize("args", [Hn.TASK_TESTS[0], Hn.TASK_TESTS[3]])
+def test_task_shapes_within_north_star_tolerance(cuda, args):
+    print(f"harness shape {args}", flush=True)
+    data = inputs.generate_input(**args)
+    out = custom_kernel(Hn.clone_data(data))
+    exp = Hn.reference_kernel(data)
+    good, msg = Hn.match(out, exp, rtol=2e-2, atol=2e-2, tol_err_ratio=0.0)
+    assert good, msg
+
+
+def test_short_leaderboard_run(cuda):
+    cases = Hn.task_cases("benchmark")[:2]
+    rc, res = Hn.run("leaderboard", cases, flush=Hn.L2Flush(64), max_repeats=4,
+                     log=lambda s: print(s, flush=True))
+    assert rc == 0
+    for st in res.values():
+        assert isinstance(st, Hn.Stats) and 3 <= st.runs <= 4 and 0 < st.best <= st.mean <= st.worst
+
+
+def test_generate_input_is_deterministic(cuda):
+    a = inputs.generate_input(4, 1, 64, 77)
+    b = inputs.generate_input(4, 1, 64, 77)
+    c = inputs.generate_input(4, 1, 64, 78)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1]["bf16"], b[1]["bf16"])
+    assert not torch.equal(a[0], c[0])
+    assert a[3].tolist() == [0, 64, 128, 192, 256] and a[4]["sm_scale"] == pytest.approx(576 ** -0.5)
+    mtp = inputs.generate_input(3, 2, 50, 5)
+    assert mtp[0].shape == (6, 16, 576) and mtp[2].tolist() == [0, 2, 4, 6]
+    ok, msg = Hn.check_implementation(mtp, custom_kernel(mtp))
+    assert ok, msg
