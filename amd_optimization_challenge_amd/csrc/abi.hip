@@ -77,19 +77,26 @@ int check_shape(int batch, int num_heads, int kv_mode) {
 // Items the planner aims for: one per resident work-group slot (H=16 fp8-V
 // kernels fit two per CU, the others one), raised to 2 per sequence when the
 // batch is large so long sequences still get split, capped at 4 rounds.
+// Resident decode work-groups per CU: two for H = 16 with the fp8 cache (a
+// two-stage ring), one otherwise (the LDS ring fills the CU).  kv_mode < 0
+// asks for the largest over the modes (the workspace is sized for it).
+static int blocks_per_cu(int num_heads, int kv_mode) {
+  if (num_heads != 16) return 1;
+  return (kv_mode == MLA_KV_FP8 || kv_mode < 0) ? 2 : 1;
+}
+
 int target_items_for(int batch, int num_heads, int kv_mode, int num_cu) {
-  (void)num_heads;
-  (void)kv_mode;
-  const int slots = num_cu;  // one resident work-group per CU (the LDS ring fills the CU)
+  const int slots = num_cu * blocks_per_cu(num_heads, kv_mode);
   int t = 2 * batch > slots ? 2 * batch : slots;
   return t < 4 * slots ? t : 4 * slots;
 }
 
 WsLayout workspace_layout(int batch, int num_heads, int kv_mode, int num_cu) {
   WsLayout L;
-  L.target_items = target_items_for(batch, num_heads, kv_mode, num_cu);
-  // the planner emits at most target + batch items; target does not depend on
-  // the kv mode, so mla_combine can recompute the layout without one
+  // the planner emits at most target + batch items; the layout is sized for the
+  // largest target over the kv modes, so mla_combine can recompute it without one
+  (void)kv_mode;
+  L.target_items = target_items_for(batch, num_heads, -1, num_cu);
   L.max_items = L.target_items + batch;
   int64_t off = 0;
   L.quant_off = off;
@@ -285,7 +292,8 @@ int mla_plan(const int32_t* kv_indptr, int batch, int q_seq_len, int num_heads, 
     return fail(MLA_ERR_WORKSPACE_TOO_SMALL, "workspace needs %lld bytes (got %lld)", (long long)L.total,
                 (long long)workspace_bytes);
   int32_t* plan = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + L.plan_off);
-  hipError_t e = launch_plan(kv_indptr, batch, q_seq_len, L.target_items, L.max_items, plan,
+  hipError_t e = launch_plan(kv_indptr, batch, q_seq_len, target_items_for(batch, num_heads, kv_mode, ncu),
+                             L.max_items, plan,
                              static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(e, "plan launch");
   return MLA_OK;
@@ -363,7 +371,8 @@ int mla_decode_fwd(const void* q_bf16, const void* k_cache, int64_t k_row_stride
   uint32_t* partials = reinterpret_cast<uint32_t*>(ws + L.quant_off);
   int nb = 0;
   hipError_t e = launch_amax(static_cast<const uint16_t*>(q_bf16), n, partials, &nb, kv_indptr,
-                             static_cast<const int32_t*>(kv_indices), batch, q_seq_len, L.target_items,
+                             static_cast<const int32_t*>(kv_indices), batch, q_seq_len,
+                             target_items_for(batch, num_heads, kv_mode, ncu),
                              L.max_items, reinterpret_cast<int32_t*>(ws + L.plan_off), s);
   if (e != hipSuccess) return hip_fail(e, "amax+plan launch");
   if (num_heads == 16) {

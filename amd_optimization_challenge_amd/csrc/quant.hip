@@ -250,7 +250,7 @@ __global__ __launch_bounds__(256) void append_kv_kernel(
 // with qlen = 1 a row is a sequence.  Below, "sequence b" means row b.
 // Sequence b is cut into n_b = max(1, ceil(L_b / chunk)) near-equal pieces.
 // For batch <= 256, chunk = the smallest multiple of 64 with sum_b n_b <=
-// target_items (binary search from c0 = max(64, 64 ceil(T / (64 target))),
+// target_items (binary search from c0 = max(128, 64 ceil(T / (64 target))),
 // T = all tokens; the longest sequence if no chunk fits), and the sequences
 // are laid out longest piece first so late-starting work-groups get the short
 // items.  For larger batches chunk = c0 and the order is the sequence order.
@@ -260,6 +260,10 @@ __global__ __launch_bounds__(256) void append_kv_kernel(
 // partial slot = its item index.
 // ---------------------------------------------------------------------------
 constexpr int kPlanSortMax = 256;
+// smallest chunk: a piece of two tiles at least, so that short batches are not
+// cut into one-tile items whose fixed costs (ring start, partial write, combine
+// input) exceed their work
+constexpr int kPlanMinChunk = 128;
 
 __device__ long long block_sum_ll(long long v, long long* red) {
 #pragma unroll
@@ -309,7 +313,7 @@ __device__ void build_plan(const int32_t* __restrict__ kv_indptr, int batch, int
   for (int b = tid; b < batch; b += 256) tsum += row_len(kv_indptr, b, qlen);
   const long long total = block_sum_ll(tsum, s_redl);
   const long long per = (total + target_items - 1) / target_items;
-  long long chunk = max(64LL, (per + 63) / 64 * 64);
+  long long chunk = max((long long)kPlanMinChunk, (per + 63) / 64 * 64);
   if (batch <= kPlanSortMax) {
     // one sequence per thread: binary search on chunk / 64 in [c0 / 64, ceil(lmax / 64)]
     const int Lt = tid < batch ? row_len(kv_indptr, tid, qlen) : 0;

@@ -281,11 +281,26 @@ def _a256(x: int) -> int:
     return (x + 255) & ~255
 
 
+def blocks_per_cu(num_heads: int, kv_mode: int) -> int:
+    """Resident decode work-groups per CU: 2 for H = 16 with the fp8 cache (two-stage
+    ring), else 1; kv_mode < 0 gives the largest over the modes."""
+    if num_heads != 16:
+        return 1
+    return 2 if kv_mode <= 0 else 1
+
+
+def target_items(batch: int, num_heads: int, kv_mode: int, num_cu: int) -> int:
+    """Work items the planner aims for (csrc/abi.hip target_items_for)."""
+    slots = num_cu * blocks_per_cu(num_heads, kv_mode)
+    return min(max(slots, 2 * batch), 4 * slots)
+
+
 def workspace_layout(batch: int, num_heads: int, kv_mode, num_cu: int) -> dict:
-    """Byte offsets of the workspace regions; ``total`` equals mla_workspace_bytes."""
+    """Byte offsets of the workspace regions; ``total`` equals mla_workspace_bytes.
+    Sized for the largest target over the kv modes (``target_items``);
+    ``plan_target`` is the one the planner uses for ``kv_mode``."""
     mode = kv_mode_id(kv_mode)
-    slots = num_cu  # one resident work-group per CU (the LDS ring fills the CU)
-    target = min(max(slots, 2 * batch), 4 * slots)
+    target = target_items(batch, num_heads, -1, num_cu)
     max_items = target + batch
     off = 0
     lay = {"quant": off}
@@ -298,7 +313,8 @@ def workspace_layout(batch: int, num_heads: int, kv_mode, num_cu: int) -> dict:
     off = _a256(off + max_items * num_heads * V_DIM * 4)
     lay["part_lse"] = off
     off = _a256(off + max_items * num_heads * 4)
-    lay.update(total=off, max_items=max_items, target_items=target)
+    lay.update(total=off, max_items=max_items, target_items=target,
+               plan_target=target_items(batch, num_heads, mode, num_cu))
     return lay
 
 

@@ -30,12 +30,13 @@ def test_plan_covers_every_token_once(cuda, lens, heads, mode):
     torch.cuda.synchronize()
     P = ops.read_plan(ws, B, heads, mode)
     assert P["batch"] == B and P["total"] == sum(lens)
-    target = P["layout"]["target_items"]
-    assert P["num_items"] <= P["max_items"] == P["layout"]["max_items"] == target + B
+    assert P["max_items"] == P["layout"]["max_items"] == P["layout"]["target_items"] + B
+    target = P["layout"]["plan_target"]
+    assert target <= P["layout"]["target_items"] and P["num_items"] <= target + B
     # B <= 256: the smallest multiple of 64 (>= c0) whose piece count fits
-    # `target` (or the longest sequence); otherwise c0 = max(64, 64 ceil(T / (64 target)))
+    # `target` (or the longest sequence); otherwise c0 = max(128, 64 ceil(T / (64 target)))
     per = -(-sum(lens) // target)
-    c0 = max(64, -(-per // 64) * 64)
+    c0 = max(128, -(-per // 64) * 64)
     count = lambda c: sum(max(1, -(-L // c)) for L in lens)
     if B <= 256:
         cands = [c for c in range(c0, max(c0, -(-max(lens) // 64) * 64) + 1, 64) if count(c) <= target]
