@@ -106,7 +106,7 @@ WsLayout workspace_layout(int batch, int num_heads, int kv_mode, int num_cu) {
   L.plan_off = off;
   off = align256(off + (int64_t)(kPlanHeader + 4 * L.max_items + 2 * batch) * 4);
   L.part_o_off = off;
-  off = align256(off + (int64_t)L.max_items * num_heads * kVDim * 4);
+  off = align256(off + (int64_t)L.max_items * num_heads * kVDim * 2);
   L.part_lse_off = off;
   off = align256(off + (int64_t)L.max_items * num_heads * 4);
   L.total = off;
@@ -164,7 +164,7 @@ int decode_params(const void* q_fp8, const float* q_scale, const void* k_cache, 
   p->kv_indptr = kv_indptr;
   p->kv_indices = kv_indices;
   p->plan = reinterpret_cast<const int32_t*>(ws + L->plan_off);
-  p->part_o = reinterpret_cast<float*>(ws + L->part_o_off);
+  p->part_o = reinterpret_cast<uint16_t*>(ws + L->part_o_off);
   p->part_lse = reinterpret_cast<float*>(ws + L->part_lse_off);
   p->out = static_cast<uint16_t*>(out);
   p->lse_out = lse_out;
@@ -329,7 +329,7 @@ int mla_combine(int batch, int num_heads, void* workspace, int64_t workspace_byt
   char* ws = static_cast<char*>(workspace);
   DecodeParams p = {};
   p.plan = reinterpret_cast<const int32_t*>(ws + L.plan_off);
-  p.part_o = reinterpret_cast<float*>(ws + L.part_o_off);
+  p.part_o = reinterpret_cast<uint16_t*>(ws + L.part_o_off);
   p.part_lse = reinterpret_cast<float*>(ws + L.part_lse_off);
   p.out = static_cast<uint16_t*>(out_bf16);
   p.lse_out = lse_out;

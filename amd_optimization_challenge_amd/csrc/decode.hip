@@ -531,12 +531,13 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
       *reinterpret_cast<uint2*>(orow + d) = make_uint2(lo, hi);
     }
   } else {
-    float* prow = p.part_o + ((int64_t)slot * 16 + head) * kVDim;
+    uint16_t* prow = p.part_o + ((int64_t)slot * 16 + head) * kVDim;
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
       const int d = 128 * w + 16 * dt + 4 * g;
-      *reinterpret_cast<float4*>(prow + d) =
-          make_float4(o[dt][0] * inv, o[dt][1] * inv, o[dt][2] * inv, o[dt][3] * inv);
+      const uint32_t lo = f32_to_bf16_bits(o[dt][0] * inv) | (f32_to_bf16_bits(o[dt][1] * inv) << 16);
+      const uint32_t hi = f32_to_bf16_bits(o[dt][2] * inv) | (f32_to_bf16_bits(o[dt][3] * inv) << 16);
+      *reinterpret_cast<uint2*>(prow + d) = make_uint2(lo, hi);
     }
     if (w == 0 && g == 0) p.part_lse[(int64_t)slot * 16 + head] = L > 0.f ? m_ref + __log2f(L) : neg_inf();
   }
@@ -890,14 +891,15 @@ __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams 
       __builtin_amdgcn_sched_barrier(0);
     }
   } else {
-    float* prow = p.part_o + ((int64_t)slot * 128 + head) * kVDim;
+    uint16_t* prow = p.part_o + ((int64_t)slot * 128 + head) * kVDim;
 #pragma unroll
     for (int dt = 0; dt < 16; ++dt) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int d = 32 * dt + 8 * q + 4 * hh;
-        *reinterpret_cast<float4*>(prow + d) = make_float4(o[dt][4 * q] * inv, o[dt][4 * q + 1] * inv,
-                                                           o[dt][4 * q + 2] * inv, o[dt][4 * q + 3] * inv);
+        const uint32_t lo = f32_to_bf16_bits(o[dt][4 * q] * inv) | (f32_to_bf16_bits(o[dt][4 * q + 1] * inv) << 16);
+        const uint32_t hi = f32_to_bf16_bits(o[dt][4 * q + 2] * inv) | (f32_to_bf16_bits(o[dt][4 * q + 3] * inv) << 16);
+        *reinterpret_cast<uint2*>(prow + d) = make_uint2(lo, hi);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -1284,14 +1286,15 @@ __global__ __launch_bounds__(256, 1) void decode_h128p_kernel(const DecodeParams
       __builtin_amdgcn_sched_barrier(0);
     }
   } else {
-    float* prow = p.part_o + ((int64_t)slot * 128 + head) * kVDim;
+    uint16_t* prow = p.part_o + ((int64_t)slot * 128 + head) * kVDim;
 #pragma unroll
     for (int dt = 0; dt < 16; ++dt) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int d = 32 * dt + 8 * q + 4 * hh;
-        *reinterpret_cast<float4*>(prow + d) = make_float4(o[dt][4 * q] * inv, o[dt][4 * q + 1] * inv,
-                                                           o[dt][4 * q + 2] * inv, o[dt][4 * q + 3] * inv);
+        const uint32_t lo = f32_to_bf16_bits(o[dt][4 * q] * inv) | (f32_to_bf16_bits(o[dt][4 * q + 1] * inv) << 16);
+        const uint32_t hi = f32_to_bf16_bits(o[dt][4 * q + 2] * inv) | (f32_to_bf16_bits(o[dt][4 * q + 3] * inv) << 16);
+        *reinterpret_cast<uint2*>(prow + d) = make_uint2(lo, hi);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -1311,7 +1314,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const DecodeParams p) {
   const int head = blockIdx.y * 16 + (threadIdx.x >> 4);
   const int d0 = blockIdx.z * 128 + (threadIdx.x & 15) * 8;
   const float* lse = p.part_lse + (int64_t)bi.x * H + head;
-  const float* po = p.part_o + ((int64_t)bi.x * H + head) * kVDim + d0;
+  const uint16_t* po = p.part_o + ((int64_t)bi.x * H + head) * kVDim + d0;
   const int64_t sstride = (int64_t)H * kVDim;
   // one pass, 8 splits per batch: lse and partial loads of a batch are issued
   // together; the running max rescales what is accumulated so far
@@ -1320,14 +1323,12 @@ __global__ __launch_bounds__(256) void combine_kernel(const DecodeParams p) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = 0.f;
   for (int s0 = 0; s0 < bi.y; s0 += 8) {
-    float4 v[8][2];
+    uint4 v[8];  // 8 bf16 of split s0 + j
     float ls[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int s = min(s0 + j, bi.y - 1);
-      const float4* src = reinterpret_cast<const float4*>(po + s * sstride);
-      v[j][0] = src[0];
-      v[j][1] = src[1];
+      v[j] = *reinterpret_cast<const uint4*>(po + s * sstride);
       ls[j] = s0 + j < bi.y ? lse[(int64_t)s * H] : neg_inf();
     }
     float mb = M;
@@ -1343,14 +1344,12 @@ __global__ __launch_bounds__(256) void combine_kernel(const DecodeParams p) {
     for (int j = 0; j < 8; ++j) {
       const float wg = exp2f(ls[j] - M);  // 0 for padding slots (lse -inf)
       wsum += wg;
-      acc[0] += wg * v[j][0].x;
-      acc[1] += wg * v[j][0].y;
-      acc[2] += wg * v[j][0].z;
-      acc[3] += wg * v[j][0].w;
-      acc[4] += wg * v[j][1].x;
-      acc[5] += wg * v[j][1].y;
-      acc[6] += wg * v[j][1].z;
-      acc[7] += wg * v[j][1].w;
+      const uint32_t wv[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc[2 * i] += wg * bf16_bits_to_f32(wv[i] & 0xFFFFu);
+        acc[2 * i + 1] += wg * bf16_bits_to_f32(wv[i] >> 16);
+      }
     }
   }
   const float inv = wsum > 0.f ? 1.0f / wsum : 0.f;

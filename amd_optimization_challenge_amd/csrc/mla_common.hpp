@@ -34,7 +34,7 @@ struct DecodeParams {
   const int32_t* kv_indptr;  // [B+1]
   const int32_t* kv_indices; // [T] or nullptr (identity)
   const int32_t* plan;       // plan block (see above)
-  float* part_o;             // [max_items, H, 512]
+  uint16_t* part_o;          // [max_items, H, 512] bf16 (normalized split outputs)
   float* part_lse;           // [max_items, H]  (log2 domain)
   uint16_t* out;             // [B, H, 512] bf16
   float* lse_out;            // [B, H] natural-log lse, or nullptr

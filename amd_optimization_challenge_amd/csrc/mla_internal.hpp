@@ -20,7 +20,7 @@ struct WsLayout {
   int64_t quant_off;   // kQuantScratchBytes: amax partials [1024] u32, q_scale f32 at +4096
   int64_t qfp8_off;    // B*H*576 bytes
   int64_t plan_off;    // (kPlanHeader + 4*max_items + 2*B) int32
-  int64_t part_o_off;  // max_items*H*512 f32
+  int64_t part_o_off;  // max_items*H*512 bf16
   int64_t part_lse_off;// max_items*H f32
   int64_t total;
   int max_items;

@@ -310,7 +310,7 @@ def workspace_layout(batch: int, num_heads: int, kv_mode, num_cu: int) -> dict:
     lay["plan"] = off
     off = _a256(off + (PLAN_HEADER + 4 * max_items + 2 * batch) * 4)
     lay["part_o"] = off
-    off = _a256(off + max_items * num_heads * V_DIM * 4)
+    off = _a256(off + max_items * num_heads * V_DIM * 2)  # bf16 split outputs
     lay["part_lse"] = off
     off = _a256(off + max_items * num_heads * 4)
     lay.update(total=off, max_items=max_items, target_items=target,
