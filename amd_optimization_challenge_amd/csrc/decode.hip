@@ -161,78 +161,6 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
 
   auto tok_of = [](int gg, int i) { return 16 * gg + i; };  // tile token of row i of wave gg's slice
 
-  // ---- Q^T (B operand): head l16, dims 128ks + 32g .. +31 -------------------
-  // With fp4 K, the f8f6f4 MFMA pairs fp4 element e of lane group g (K =
-  // 32g + e within the 128-step, one MX block) with fp8 byte i of lane group
-  // g' where 32g + e = 16g' + (i & 15) + 64 (i >> 4); the fp8 Q operand is
-  // gathered in that order.  With fp8 K both operands share one order.
-  v8i qv[5];
-  float qs;
-  {
-    auto load_q = [&](const uint8_t* qrow) {
-      if constexpr (KF == 0) {
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) qv[ks] = ld_v8(qrow + 128 * ks + 32 * g);
-        qv[4] = g < 2 ? ld_v8(qrow + 512 + 32 * g) : v8i{0, 0, 0, 0, 0, 0, 0, 0};
-      } else {
-#pragma unroll
-        for (int ks = 0; ks < 5; ++ks) {
-          const uint4 lo = *reinterpret_cast<const uint4*>(qrow + 128 * ks + 16 * g);
-          const uint4 hi = ks < 4 ? *reinterpret_cast<const uint4*>(qrow + 128 * ks + 64 + 16 * g)
-                                  : make_uint4(0, 0, 0, 0);
-          qv[ks] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-        }
-      }
-    };
-    if constexpr (QB) {
-      // Q quantized here (bit-exact with the quant kernel): the per-tensor
-      // scale is folded from the amax partials, and this sequence's 16 x 576
-      // fp8 Q is staged row-major in the last ring stage (its first DMA comes
-      // after the first tile barrier)
-      uint8_t* qst = smem + (C::S - 1) * C::STAGE;
-      const uint4* src = reinterpret_cast<const uint4*>(p.q_bf16 + (int64_t)b * 16 * kQKDim);
-      constexpr int NV = 16 * kQKDim / 8, NJ = (NV + 255) / 256;
-      uint4 xv[NJ];
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        const int i = tid + 256 * j;
-        if (i < NV) xv[j] = src[i];
-      }
-      uint32_t m = 0;
-      for (int i = tid; i < p.q_nparts; i += 256) m = max(m, p.q_partials[i]);
-#pragma unroll
-      for (int off = 32; off > 0; off >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, off, 64));
-      uint32_t* xu = reinterpret_cast<uint32_t*>(smem + C::OFF_X);
-      if (lane == 0) xu[w] = m;
-      lds_barrier();
-      qs = fp8_scale_from_amax(max(max(xu[0], xu[1]), max(xu[2], xu[3])));
-      const Fp8Quant qq = make_fp8_quant(qs);
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        const int i = tid + 256 * j;
-        if (i < NV) {
-          *reinterpret_cast<uint2*>(qst + 8 * i) = quant8_fp8(xv[j], qq);
-        }
-      }
-      lds_barrier();
-      load_q(qst + l16 * kQKDim);
-    } else {
-      qs = p.q_scale[0];
-      load_q(p.q_fp8 + ((int64_t)b * 16 + l16) * kQKDim);
-    }
-#pragma unroll
-    for (int ks = 0; ks < 5; ++ks) asm volatile("" : "+v"(qv[ks]));  // keep resident, no reload
-  }
-  const float kvs = (KF == 0 || VF == 1) ? p.kv_scale[0] : 1.0f;
-  const float c = qs * (KF == 0 ? kvs : 1.0f) * p.sm_scale * kLog2e;
-  const float vscale = VF == 2 ? 1.0f : kvs;
-
-  v4f o[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) o[i] = v4f{0.f, 0.f, 0.f, 0.f};
-  float m_ref = 0.f, m_seen = neg_inf(), l_part = 0.f;
-  bool have_ref = false;
-
   // ---- ring issue ----------------------------------------------------------
   // slots of tile t live in slot stage t % NSL
   auto slot_of = [&](int t, int tok) -> int {
@@ -305,9 +233,89 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
   // group x = {slots(x + S - 1), rows(x) | scales(x)}, issued S - 1 tiles
   // ahead of the tile x compute: once a group has landed, so have the slots
   // the rows of group x + S - 1 need
-  auto prologue = [&]() {
+  // the first slot indices are in flight while Q is loaded (and quantized)
+  if (ntiles > 0) {
 #pragma unroll
     for (int j = 0; j < C::S - 1; ++j) issue_slots(j);
+  }
+
+  // ---- Q^T (B operand): head l16, dims 128ks + 32g .. +31 -------------------
+  // With fp4 K, the f8f6f4 MFMA pairs fp4 element e of lane group g (K =
+  // 32g + e within the 128-step, one MX block) with fp8 byte i of lane group
+  // g' where 32g + e = 16g' + (i & 15) + 64 (i >> 4); the fp8 Q operand is
+  // gathered in that order.  With fp8 K both operands share one order.
+  v8i qv[5];
+  float qs;
+  {
+    auto load_q = [&](const uint8_t* qrow) {
+      if constexpr (KF == 0) {
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) qv[ks] = ld_v8(qrow + 128 * ks + 32 * g);
+        qv[4] = g < 2 ? ld_v8(qrow + 512 + 32 * g) : v8i{0, 0, 0, 0, 0, 0, 0, 0};
+      } else {
+#pragma unroll
+        for (int ks = 0; ks < 5; ++ks) {
+          const uint4 lo = *reinterpret_cast<const uint4*>(qrow + 128 * ks + 16 * g);
+          const uint4 hi = ks < 4 ? *reinterpret_cast<const uint4*>(qrow + 128 * ks + 64 + 16 * g)
+                                  : make_uint4(0, 0, 0, 0);
+          qv[ks] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+        }
+      }
+    };
+    if constexpr (QB) {
+      // Q quantized here (bit-exact with the quant kernel): the per-tensor
+      // scale is folded from the amax partials, and this sequence's 16 x 576
+      // fp8 Q is staged row-major in the last ring stage (its first DMA comes
+      // after the first tile barrier)
+      uint8_t* qst = smem + (C::S - 1) * C::STAGE;
+      const uint4* src = reinterpret_cast<const uint4*>(p.q_bf16 + (int64_t)b * 16 * kQKDim);
+      constexpr int NV = 16 * kQKDim / 8, NJ = (NV + 255) / 256;
+      uint4 xv[NJ];
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const int i = tid + 256 * j;
+        if (i < NV) xv[j] = src[i];
+      }
+      uint32_t m = 0;
+      for (int i = tid; i < p.q_nparts; i += 256) m = max(m, p.q_partials[i]);
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, off, 64));
+      uint32_t* xu = reinterpret_cast<uint32_t*>(smem + C::OFF_X);
+      if (lane == 0) xu[w] = m;
+      lds_barrier();
+      qs = fp8_scale_from_amax(max(max(xu[0], xu[1]), max(xu[2], xu[3])));
+      const Fp8Quant qq = make_fp8_quant(qs);
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const int i = tid + 256 * j;
+        if (i < NV) {
+          *reinterpret_cast<uint2*>(qst + 8 * i) = quant8_fp8(xv[j], qq);
+        }
+      }
+      lds_barrier();
+      load_q(qst + l16 * kQKDim);
+    } else {
+      qs = p.q_scale[0];
+      load_q(p.q_fp8 + ((int64_t)b * 16 + l16) * kQKDim);
+    }
+#pragma unroll
+    for (int ks = 0; ks < 5; ++ks) asm volatile("" : "+v"(qv[ks]));  // keep resident, no reload
+  }
+  const float kvs = (KF == 0 || VF == 1) ? p.kv_scale[0] : 1.0f;
+  const float c = qs * (KF == 0 ? kvs : 1.0f) * p.sm_scale * kLog2e;
+  const float vscale = VF == 2 ? 1.0f : kvs;
+
+  v4f o[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) o[i] = v4f{0.f, 0.f, 0.f, 0.f};
+  float m_ref = 0.f, m_seen = neg_inf(), l_part = 0.f;
+  bool have_ref = false;
+
+  auto prologue = [&](bool slots_issued) {
+    if (!slots_issued) {
+#pragma unroll
+      for (int j = 0; j < C::S - 1; ++j) issue_slots(j);
+    }
     wait_vmcnt<0>();
     lds_barrier();
 #pragma unroll
@@ -322,9 +330,11 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
   // ---- main loop ---------------------------------------------------------------
   int8_t* vote = reinterpret_cast<int8_t*>(smem + C::OFF_VOTE);
   float* xch = reinterpret_cast<float*>(smem + C::OFF_X);
+  bool slots_issued = true;  // by the early issue above; a restart issues them again
   for (;;) {
     bool restart = false;
-    if (ntiles > 0) prologue();
+    if (ntiles > 0) prologue(slots_issued);
+    slots_issued = false;
     for (int ti = 0; ti < ntiles; ++ti) {
       const int st = ti % C::S;
       const int nval = min(kTile, ntok - kTile * ti);

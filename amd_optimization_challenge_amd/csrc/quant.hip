@@ -302,8 +302,94 @@ __device__ __forceinline__ int row_len(const int32_t* __restrict__ kv_indptr, in
   return max(kv_indptr[b + 1] - kv_indptr[b] - (qlen - 1 - i), 0);
 }
 
+// the nb near-equal pieces of [s0, s0 + L): piece i = [s0 + floor(iL/nb),
+// s0 + floor((i+1)L/nb)), computed with one division and a running remainder
+__device__ __forceinline__ void emit_pieces(int4* __restrict__ items, int b, int s0, int L, int nb, int first) {
+  const int q = L / nb, r = L - q * nb;
+  int t = s0, rem = 0;
+  for (int i = 0; i < nb; ++i) {
+    int t1 = t + q;
+    rem += r;
+    if (rem >= nb) {
+      rem -= nb;
+      ++t1;
+    }
+    items[first + i] = make_int4(b, t, t1, nb > 1 ? first + i : -1);
+    t = t1;
+  }
+}
+
+// Up to 64 rows: one wave plans alone, with every reduction, the binary
+// search and the ordering in registers (shuffles; ds_permute to scatter each
+// row's item count to its rank position and ds_bpermute to gather its first
+// item back), so the plan costs one round trip to kv_indptr and no barriers.
+// Same plan as the block version below.
+__device__ void build_plan_wave(const int32_t* __restrict__ kv_indptr, int batch, int qlen, int target_items,
+                                int max_items, int32_t* __restrict__ plan) {
+  const int lane = threadIdx.x & 63;
+  const bool act = lane < batch;
+  const int s0 = act ? row_start(kv_indptr, lane, qlen) : 0;
+  const int L = act ? row_len(kv_indptr, lane, qlen) : 0;
+  long long total = L;
+  int lmax = L;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    total += __shfl_xor(total, off, 64);
+    lmax = max(lmax, __shfl_xor(lmax, off, 64));
+  }
+  const long long per = (total + target_items - 1) / target_items;
+  int lo = (int)(max((long long)kPlanMinChunk, (per + 63) / 64 * 64) / 64);
+  int hi = max(lo, (lmax + 63) / 64);
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    const int c = mid * 64;
+    int cnt = act ? (L > 0 ? (L + c - 1) / c : 1) : 0;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) cnt += __shfl_xor(cnt, off, 64);
+    if (cnt <= target_items) hi = mid;
+    else lo = mid + 1;
+  }
+  const int chunk = lo * 64;
+  const int nb = act ? (L > 0 ? (L + chunk - 1) / chunk : 1) : 0;
+  const int piece = act ? (L > 0 ? (L + nb - 1) / nb : 0) : -1;
+  // rank by piece length, longest first (ties by index); inactive lanes rank last
+  int rank = 0;
+  for (int b2 = 0; b2 < batch; ++b2) {
+    const int p2 = __shfl(piece, b2, 64);
+    rank += (p2 > piece) || (p2 == piece && b2 < lane);
+  }
+  if (!act) rank = lane;
+  // item counts in rank order -> exclusive scan -> each row's first item
+  const int by_rank = __builtin_amdgcn_ds_permute(rank << 2, nb);
+  int x = by_rank;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(x, off, 64);
+    if (lane >= off) x += y;
+  }
+  const int n_items = __shfl(x, 63, 64);
+  const int first = __builtin_amdgcn_ds_bpermute(rank << 2, x - by_rank);
+  if (act) {
+    int4* items = reinterpret_cast<int4*>(plan + kPlanHeader);
+    int2* binfo = reinterpret_cast<int2*>(plan + kPlanHeader + 4 * max_items);
+    binfo[lane] = make_int2(first, nb);
+    emit_pieces(items, lane, s0, L, nb, first);
+  }
+  if (lane == 0) {
+    plan[0] = n_items;
+    plan[1] = chunk;
+    plan[2] = (int)total;
+    plan[3] = batch;
+    plan[4] = max_items;
+  }
+}
+
 __device__ void build_plan(const int32_t* __restrict__ kv_indptr, int batch, int qlen, int target_items,
                            int max_items, int32_t* __restrict__ plan) {
+  if (batch <= 64) {
+    if (threadIdx.x < 64) build_plan_wave(kv_indptr, batch, qlen, target_items, max_items, plan);
+    return;
+  }
   __shared__ long long s_redl[4];
   __shared__ int s_red[4];
   __shared__ int s_piece[kPlanSortMax];  // piece length per sequence
@@ -341,11 +427,7 @@ __device__ void build_plan(const int32_t* __restrict__ kv_indptr, int batch, int
   auto emit = [&](int b, int L, int nb, int first) {
     const int s0 = row_start(kv_indptr, b, qlen);
     binfo[b] = make_int2(first, nb);
-    for (int i = 0; i < nb; ++i) {
-      const int t0 = s0 + (int)(((long long)i * L) / nb);
-      const int t1 = s0 + (int)(((long long)(i + 1) * L) / nb);
-      items[first + i] = make_int4(b, t0, t1, nb > 1 ? first + i : -1);
-    }
+    emit_pieces(items, b, s0, L, nb, first);
   };
   int carry = 0;
   if (batch <= kPlanSortMax) {
