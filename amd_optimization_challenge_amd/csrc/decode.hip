@@ -278,8 +278,7 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
       }
       uint32_t m = 0;
       for (int i = tid; i < p.q_nparts; i += 256) m = max(m, p.q_partials[i]);
-#pragma unroll
-      for (int off = 32; off > 0; off >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, off, 64));
+      m = (uint32_t)wave_max((int)m);
       uint32_t* xu = reinterpret_cast<uint32_t*>(smem + C::OFF_X);
       if (lane == 0) xu[w] = m;
       lds_barrier();

@@ -221,6 +221,33 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 // Work-group barrier for LDS only (no global-memory fence, so outstanding
 // DMA/prefetch loads are not drained).
+// Wave-wide inclusive prefix sum in lane order: a Hillis-Steele scan inside
+// each 16-lane row by DPP row shifts (lanes shifted in from outside the row read
+// 0), then the row totals carried forward by the gfx9 row broadcasts (lane 15
+// of rows 0 and 2 into rows 1 and 3, lane 31 into rows 2 and 3).  Six VALU ops,
+// no LDS round trips.
+__device__ __forceinline__ int wave_incl_sum(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, true);   // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, true);   // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, true);   // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, true);   // row_shr:8
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);  // row_bcast:15
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);  // row_bcast:31
+  return x;
+}
+// the same pattern with max, for non-negative values; lane 63 holds the wave max
+__device__ __forceinline__ int wave_incl_max(int x) {
+  x = max(x, __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, true));
+  x = max(x, __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, true));
+  x = max(x, __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, true));
+  x = max(x, __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, true));
+  x = max(x, __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false));
+  x = max(x, __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false));
+  return x;
+}
+__device__ __forceinline__ int wave_sum(int x) { return __builtin_amdgcn_readlane(wave_incl_sum(x), 63); }
+__device__ __forceinline__ int wave_max(int x) { return __builtin_amdgcn_readlane(wave_incl_max(x), 63); }
+
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // ds_read_b64_tr_b8: within each 16-lane group, result lane j gets byte (j & 7)

@@ -57,9 +57,8 @@ __global__ __launch_bounds__(256) void amax_kernel(const uint16_t* __restrict__ 
   for (int64_t i = (nvec << 3) + (int64_t)blockIdx.x * 256 + threadIdx.x; i < n;
        i += (int64_t)nblocks * 256)
     m = max(m, (uint32_t)(x[i] & 0x7FFFu));
-  // wave reduce then block reduce
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, off, 64));
+  // wave reduce (DPP) then block reduce
+  m = (uint32_t)wave_max((int)m);
   __shared__ uint32_t red[4];
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
   __syncthreads();
@@ -74,8 +73,7 @@ __global__ __launch_bounds__(256) void quant_fp8_kernel(const uint16_t* __restri
   __shared__ uint32_t red[4];
   uint32_t m = 0;
   for (int i = threadIdx.x; i < nparts; i += 256) m = max(m, partials[i]);
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, off, 64));
+  m = (uint32_t)wave_max((int)m);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
   __syncthreads();
   if (threadIdx.x == 0) {
@@ -230,8 +228,7 @@ __global__ __launch_bounds__(256) void append_kv_kernel(
     // one atomic per block at most, and only when it raises the stored max:
     // atomics on one address serialize, so per-wave atomics would dominate
     __shared__ uint32_t red[4];
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) amax = max(amax, (uint32_t)__shfl_xor((int)amax, off, 64));
+    amax = (uint32_t)wave_max((int)amax);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -265,25 +262,28 @@ constexpr int kPlanSortMax = 256;
 // input) exceed their work
 constexpr int kPlanMinChunk = 128;
 
-__device__ long long block_sum_ll(long long v, long long* red) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+// sum / max of one non-negative int per thread over the 256-thread block
+// (`red` holds 4 ints; every thread gets the result)
+__device__ int block_sum(int v, int* red) {
+  const int t = wave_sum(v);
+  __syncthreads();  // red free
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = t;
   __syncthreads();
   return red[0] + red[1] + red[2] + red[3];
+}
+__device__ int block_max(int v, int* red) {
+  const int t = wave_max(v);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = t;
+  __syncthreads();
+  return max(max(red[0], red[1]), max(red[2], red[3]));
 }
 
 // exclusive scan of one int per thread over the 256-thread block; *total =
 // the block sum (same in every thread)
 __device__ int block_exscan(int v, int* red, int* total) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  int x = v;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int y = __shfl_up(x, off, 64);
-    if (lane >= off) x += y;
-  }
+  const int x = wave_incl_sum(v);
   __syncthreads();  // red free
   if (lane == 63) red[w] = x;
   __syncthreads();
@@ -291,6 +291,16 @@ __device__ int block_exscan(int v, int* red, int* total) {
   for (int i = 0; i < w; ++i) base += red[i];
   *total = red[0] + red[1] + red[2] + red[3];
   return base + x - v;
+}
+
+// ceil(total / (64 target)) for total = 64 s1 + s0 (the sums of L >> 6 and of
+// L & 63 over the rows), in 32-bit arithmetic: ceil(total / 64) = s1 +
+// ceil(s0 / 64), and nested ceilings of integer quotients compose.  Valid while
+// the sum of L over all rows stays below 2^37 (s1 < 2^31) and there are fewer
+// than 2^25 rows (s0 < 2^31).
+__device__ __forceinline__ unsigned tiles_per_item(unsigned s1, unsigned s0, int target) {
+  const unsigned t64 = s1 + (s0 + 63u) / 64u;
+  return (t64 + (unsigned)target - 1u) / (unsigned)target;
 }
 
 // first key token and key count of query row r
@@ -330,44 +340,32 @@ __device__ void build_plan_wave(const int32_t* __restrict__ kv_indptr, int batch
   const bool act = lane < batch;
   const int s0 = act ? row_start(kv_indptr, lane, qlen) : 0;
   const int L = act ? row_len(kv_indptr, lane, qlen) : 0;
-  long long total = L;
-  int lmax = L;
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    total += __shfl_xor(total, off, 64);
-    lmax = max(lmax, __shfl_xor(lmax, off, 64));
-  }
-  const long long per = (total + target_items - 1) / target_items;
-  int lo = (int)(max((long long)kPlanMinChunk, (per + 63) / 64 * 64) / 64);
+  const unsigned hi64 = (unsigned)wave_sum(L >> 6), lo64 = (unsigned)wave_sum(L & 63);
+  const int lmax = wave_max(L);
+  int lo = max(kPlanMinChunk / 64, (int)tiles_per_item(hi64, lo64, target_items));
   int hi = max(lo, (lmax + 63) / 64);
+  const int L64 = (L + 63) >> 6;  // ceil(L / (64 m)) = ceil(L64 / m)
   while (lo < hi) {
     const int mid = (lo + hi) >> 1;
-    const int c = mid * 64;
-    int cnt = act ? (L > 0 ? (L + c - 1) / c : 1) : 0;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) cnt += __shfl_xor(cnt, off, 64);
+    const int cnt = wave_sum(act ? (L64 > 0 ? (L64 + mid - 1) / mid : 1) : 0);
     if (cnt <= target_items) hi = mid;
     else lo = mid + 1;
   }
   const int chunk = lo * 64;
-  const int nb = act ? (L > 0 ? (L + chunk - 1) / chunk : 1) : 0;
+  const int nb = act ? (L > 0 ? (L64 + lo - 1) / lo : 1) : 0;
   const int piece = act ? (L > 0 ? (L + nb - 1) / nb : 0) : -1;
-  // rank by piece length, longest first (ties by index); inactive lanes rank last
+  // rank by piece length, longest first (ties by index); inactive lanes rank
+  // last.  The pieces are read lane by lane into scalar registers.
   int rank = 0;
   for (int b2 = 0; b2 < batch; ++b2) {
-    const int p2 = __shfl(piece, b2, 64);
+    const int p2 = __builtin_amdgcn_readlane(piece, b2);
     rank += (p2 > piece) || (p2 == piece && b2 < lane);
   }
   if (!act) rank = lane;
   // item counts in rank order -> exclusive scan -> each row's first item
   const int by_rank = __builtin_amdgcn_ds_permute(rank << 2, nb);
-  int x = by_rank;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int y = __shfl_up(x, off, 64);
-    if (lane >= off) x += y;
-  }
-  const int n_items = __shfl(x, 63, 64);
+  const int x = wave_incl_sum(by_rank);
+  const int n_items = __builtin_amdgcn_readlane(x, 63);
   const int first = __builtin_amdgcn_ds_bpermute(rank << 2, x - by_rank);
   if (act) {
     int4* items = reinterpret_cast<int4*>(plan + kPlanHeader);
@@ -378,7 +376,7 @@ __device__ void build_plan_wave(const int32_t* __restrict__ kv_indptr, int batch
   if (lane == 0) {
     plan[0] = n_items;
     plan[1] = chunk;
-    plan[2] = (int)total;
+    plan[2] = (int)(64u * hi64 + lo64);
     plan[3] = batch;
     plan[4] = max_items;
   }
@@ -390,38 +388,34 @@ __device__ void build_plan(const int32_t* __restrict__ kv_indptr, int batch, int
     if (threadIdx.x < 64) build_plan_wave(kv_indptr, batch, qlen, target_items, max_items, plan);
     return;
   }
-  __shared__ long long s_redl[4];
   __shared__ int s_red[4];
   __shared__ int s_piece[kPlanSortMax];  // piece length per sequence
   __shared__ int s_cnt[kPlanSortMax];    // item counts in layout order, then their exclusive scan
   const int tid = threadIdx.x;
-  long long tsum = 0;
-  for (int b = tid; b < batch; b += 256) tsum += row_len(kv_indptr, b, qlen);
-  const long long total = block_sum_ll(tsum, s_redl);
-  const long long per = (total + target_items - 1) / target_items;
-  long long chunk = max((long long)kPlanMinChunk, (per + 63) / 64 * 64);
+  int t_hi = 0, t_lo = 0, t_max = 0;
+  for (int b = tid; b < batch; b += 256) {
+    const int L = row_len(kv_indptr, b, qlen);
+    t_hi += L >> 6;
+    t_lo += L & 63;
+    t_max = max(t_max, L);
+  }
+  const unsigned hi64 = (unsigned)block_sum(t_hi, s_red), lo64 = (unsigned)block_sum(t_lo, s_red);
+  int chunk = 64 * max(kPlanMinChunk / 64, (int)tiles_per_item(hi64, lo64, target_items));
   if (batch <= kPlanSortMax) {
     // one sequence per thread: binary search on chunk / 64 in [c0 / 64, ceil(lmax / 64)]
-    const int Lt = tid < batch ? row_len(kv_indptr, tid, qlen) : 0;
-    long long lm = Lt;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) lm = max(lm, (long long)__shfl_xor(lm, off, 64));
-    __syncthreads();
-    if ((tid & 63) == 0) s_redl[tid >> 6] = lm;
-    __syncthreads();
-    const long long lmax = max(max(s_redl[0], s_redl[1]), max(s_redl[2], s_redl[3]));
-    long long lo = chunk / 64, hi = max(lo, (lmax + 63) / 64);
+    const int lmax = block_max(t_max, s_red);
+    const int L64 = (t_max + 63) >> 6;  // batch <= 256: t_max is this thread's own L
+    int lo = chunk / 64, hi = max(lo, (lmax + 63) / 64);
     while (lo < hi) {
-      const long long mid = (lo + hi) >> 1;
-      const long long c = mid * 64;
-      const long long cnt = block_sum_ll(tid < batch ? (Lt > 0 ? (Lt + c - 1) / c : 1) : 0, s_redl);
+      const int mid = (lo + hi) >> 1;
+      const int cnt = block_sum(tid < batch ? (L64 > 0 ? (L64 + mid - 1) / mid : 1) : 0, s_red);
       if (cnt <= target_items) hi = mid;
       else lo = mid + 1;
     }
     chunk = lo * 64;
   }
   auto len_of = [&](int b) { return row_len(kv_indptr, b, qlen); };
-  auto nb_of = [&](int L) { return L > 0 ? (int)((L + chunk - 1) / chunk) : 1; };
+  auto nb_of = [&](int L) { return L > 0 ? (L + chunk - 1) / chunk : 1; };
   int4* items = reinterpret_cast<int4*>(plan + kPlanHeader);
   int2* binfo = reinterpret_cast<int2*>(plan + kPlanHeader + 4 * max_items);
   auto emit = [&](int b, int L, int nb, int first) {
@@ -472,8 +466,8 @@ __device__ void build_plan(const int32_t* __restrict__ kv_indptr, int batch, int
   }
   if (tid == 0) {
     plan[0] = carry;
-    plan[1] = (int)chunk;
-    plan[2] = (int)total;
+    plan[1] = chunk;
+    plan[2] = (int)(64u * hi64 + lo64);
     plan[3] = batch;
     plan[4] = max_items;
   }

@@ -14,6 +14,12 @@ CASES = [
     [1] * 300,
     [32768] * 3 + [1] * 100,
     [8192, 512, 4096, 777, 3, 20000],
+    # the one-wave planner at its limit and the block planner just past it,
+    # with lengths that make every DPP row and row broadcast carry
+    [(i * 7919) % 9000 + (i % 5) * 64 for i in range(64)],
+    [(i * 7919) % 9000 + 1 for i in range(65)],
+    [(i * 104729) % 33000 for i in range(256)],
+    [(i * 37) % 2000 for i in range(257)],
 ]
 
 
