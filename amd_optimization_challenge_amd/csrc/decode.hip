@@ -81,7 +81,7 @@ __device__ __forceinline__ void pack4_fp8_split(float a, float b, float c, float
 }
 
 // waits until at most k groups of PER operations issued after the one waited
-// for are still outstanding (k in 0..2, the ring depth minus two)
+// for are still outstanding (k in 0..2: at most the ring depth minus one, S <= 3)
 template <int PER>
 __device__ __forceinline__ void wait_groups(int k) {
   if (k <= 0) wait_vmcnt<0>();
@@ -129,7 +129,7 @@ struct H16 {
   static constexpr int NAW = NW % NRW == 0 ? NRW : NW % NRW;   // row waves (from RW0) that issue NA
   static constexpr bool VB16 = VF == 2;
   static constexpr int VTST = 144;                             // bf16 V^T / P^T row stride
-  static constexpr int NSL = 2 * S;                            // slot stages (slots lead rows by S - 1 tiles)
+  static constexpr int NSL = 2 * S;                            // slot stages (slots lead rows by S tiles)
   static constexpr int OFF_SLOT = S * STAGE;                   // [NSL][64] int32 cache slots
   static constexpr int SCST = kMxBlocks * 256;                 // e8m0 stage: [18 blocks][64 tokens] dwords
   static constexpr int OFF_SC = OFF_SLOT + NSL * 256;          // [S] e8m0 stages (KF == 1)
@@ -230,13 +230,16 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
       else wait_groups<C::NA - 1>(k);
     }
   };
-  // group x = {slots(x + S - 1), rows(x) | scales(x)}, issued S - 1 tiles
-  // ahead of the tile x compute: once a group has landed, so have the slots
-  // the rows of group x + S - 1 need
-  // the first slot indices are in flight while Q is loaded (and quantized)
+  // group x = {slots(x + S), rows(x) | scales(x)}.  The prologue issues groups
+  // 0 .. S-1 (every stage is free then, so the first S tiles are in flight
+  // together: a short item pays one row round trip, not one per tile); the
+  // pass of tile t >= 1 issues group t + S - 1 into the stage tile t - 1 used.
+  // The slots of tile x arrive with group x - S (the prologue's wait covers
+  // tiles 0 .. S-1), one barrier before the rows that read them are issued.
+  // The first slot indices are in flight while Q is loaded (and quantized).
   if (ntiles > 0) {
 #pragma unroll
-    for (int j = 0; j < C::S - 1; ++j) issue_slots(j);
+    for (int j = 0; j < C::S; ++j) issue_slots(j);
   }
 
   // ---- Q^T (B operand): head l16, dims 128ks + 32g .. +31 -------------------
@@ -313,14 +316,14 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
   auto prologue = [&](bool slots_issued) {
     if (!slots_issued) {
 #pragma unroll
-      for (int j = 0; j < C::S - 1; ++j) issue_slots(j);
+      for (int j = 0; j < C::S; ++j) issue_slots(j);
     }
     wait_vmcnt<0>();
     lds_barrier();
 #pragma unroll
-    for (int j = 0; j < C::S - 1; ++j) {
+    for (int j = 0; j < C::S; ++j) {
       if (j >= ntiles) break;
-      issue_slots(j + C::S - 1);
+      issue_slots(j + C::S);
       issue_rows(j);
       issue_scales(j);
     }
@@ -337,10 +340,12 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
     for (int ti = 0; ti < ntiles; ++ti) {
       const int st = ti % C::S;
       const int nval = min(kTile, ntok - kTile * ti);
-      wait_tile(min(C::S - 2, ntiles - 1 - ti));
+      // groups issued after group ti: 1 .. S-1 at the first tile, then the
+      // S-2 before this pass's own issue
+      wait_tile(min(ti == 0 ? C::S - 1 : C::S - 2, ntiles - 1 - ti));
       lds_barrier();  // (1) tile ti and its scales visible; iteration ti-1 done everywhere
-      if (ti + C::S - 1 < ntiles) {
-        issue_slots(ti + 2 * C::S - 2);
+      if (ti >= 1 && ti + C::S - 1 < ntiles) {
+        issue_slots(ti + 2 * C::S - 1);
         issue_rows(ti + C::S - 1);
         issue_scales(ti + C::S - 1);
       }
