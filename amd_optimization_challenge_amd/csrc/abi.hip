@@ -80,9 +80,11 @@ int check_shape(int batch, int num_heads, int kv_mode) {
 // Resident decode work-groups per CU: two for H = 16 with the fp8 cache (a
 // two-stage ring), one otherwise (the LDS ring fills the CU).  kv_mode < 0
 // asks for the largest over the modes (the workspace is sized for it).
+// resident decode work-groups per CU: 2 for H = 16 with one cache (fp8 or
+// mxfp4 rows serve both K and V), else 1; kv_mode < 0 gives the largest
 static int blocks_per_cu(int num_heads, int kv_mode) {
   if (num_heads != 16) return 1;
-  return (kv_mode == MLA_KV_FP8 || kv_mode < 0) ? 2 : 1;
+  return (kv_mode == MLA_KV_FP8 || kv_mode == MLA_KV_MXFP4 || kv_mode < 0) ? 2 : 1;
 }
 
 int target_items_for(int batch, int num_heads, int kv_mode, int num_cu) {

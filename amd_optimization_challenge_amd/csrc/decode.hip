@@ -65,6 +65,13 @@ __device__ __forceinline__ uint32_t cvt_fp4_byte(uint32_t word, float scale) {
   return __builtin_bit_cast(uint32_t, r);
 }
 
+// two floats -> bf16 pair (RNE, v_cvt_pk_bf16_f32), a in the low half
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  typedef __bf16 v2bf_t __attribute__((ext_vector_type(2)));
+  const v2bf_t r = {(__bf16)a, (__bf16)b};
+  return __builtin_bit_cast(uint32_t, r);
+}
+
 __device__ __forceinline__ float e8m0_to_f32(uint32_t e) {
   return e == 0 ? __uint_as_float(0x00400000u) : __uint_as_float(e << 23);
 }
@@ -101,10 +108,16 @@ __device__ __forceinline__ void wait_groups(int k) {
 // head, m_ref a per-item reference, so no cross-wave max and no rescale of
 // O^T per tile.  The A operand (V^T) comes from the row-major tile through
 // ds_read_b64_tr_b8; K block g of the MFMA holds wave g's 16 tokens (+16 zeros).
-// fp4 V: the tile is dequantized to a bf16 V^T in LDS and P = 2^(s - m_ref) is
-// bf16; PV runs on 16x16x32 bf16 MFMAs.
-// A tile max more than kRebase above m_ref restarts the item from a higher
-// reference (block-wide vote), so the accumulators cannot overflow.
+// fp4 V: no dequantized copy of the tile.  Each wave reads its V^T fragments
+// straight from the packed rows with ds_read_b64_tr_b4 (16 tokens of one latent
+// dim per lane), widens the e2m1 codes to bf16 unscaled, and folds each token's
+// e8m0 block scale into P instead: P'_j = P * 2^(e[t, j] - E_ref) for MX block j,
+// with P = 2^(s - m_ref) in f32 shared through LDS and E_ref a per-item
+// reference exponent; O^T is rescaled by 2^(E_ref - 127) at the end.  PV runs on
+// 16x16x32 bf16 MFMAs.  The LDS this frees lets two work-groups share a CU.
+// A tile max more than kRebase above m_ref, or (fp4 V) a V block exponent more
+// than kVScaleSpan above E_ref, restarts the item from a higher reference
+// (block-wide vote), so neither the accumulators nor P' can overflow.
 // ============================================================================
 template <int KF, int VF>
 struct H16 {
@@ -117,30 +130,34 @@ struct H16 {
   static constexpr int VW = VF == 1 ? kTile * VST / 1024 : 0;  // of V rows: 33
   static constexpr int NW = KW + VW;
   static constexpr int STAGE = NW * 1024;
-  // ring depth (tiles).  fp8 K = V: two stages, so two work-groups share a CU
-  // (LDS ~79 KiB, <= 256 registers a wave) and their eight waves keep twice the
-  // row gathers in flight; fp4 K needs its bf16 V^T or scale stages and runs
-  // one work-group per CU.
+  // ring depth (tiles).  fp8 K = V: two stages; fp4 K = V: three stages of rows
+  // and scales.  Both fit two work-groups per CU (LDS <= 80 KiB, <= 256
+  // registers a wave), whose eight waves keep twice the row gathers in flight
+  // and overlap one group's compute with the other's waits.  fp4 K + fp8 V
+  // (two caches) runs one work-group per CU.
   static constexpr int S = KF == 0 ? 2 : (VF == 1 ? 2 : 3);
-  static constexpr int BLOCKS_PER_CU = KF == 0 ? 2 : 1;
+  static constexpr int BLOCKS_PER_CU = VF == 1 ? 1 : 2;
   static constexpr int RW0 = KF == 1 ? 1 : 0;                  // waves RW0..3 DMA rows; wave 0 the scales
   static constexpr int NRW = 4 - RW0;
   static constexpr int NA = (NW + NRW - 1) / NRW;              // windows per row wave: NA or NA - 1
   static constexpr int NAW = NW % NRW == 0 ? NRW : NW % NRW;   // row waves (from RW0) that issue NA
-  static constexpr bool VB16 = VF == 2;
-  static constexpr int VTST = 144;                             // bf16 V^T / P^T row stride
+  static constexpr bool VB16 = VF == 2;                        // fp4 V, bf16 PV from registers
+  static constexpr int PST = 68;                               // f32 P row stride (VB16): 64 tokens + 4
   static constexpr int NSL = 2 * S;                            // slot stages (slots lead rows by S tiles)
   static constexpr int OFF_SLOT = S * STAGE;                   // [NSL][64] int32 cache slots
   static constexpr int SCST = kMxBlocks * 256;                 // e8m0 stage: [18 blocks][64 tokens] dwords
   static constexpr int OFF_SC = OFF_SLOT + NSL * 256;          // [S] e8m0 stages (KF == 1)
-  static constexpr int OFF_VT = OFF_SC + (KF == 1 ? S * SCST : 0);
-  static constexpr int OFF_P = OFF_VT + (VB16 ? kVDim * VTST : 0);
-  static constexpr int P_BYTES = VB16 ? 16 * VTST : 2 * 4 * 16 * 16;  // bf16 [h][pos] | fp8 [term][g][h][16]
+  static constexpr int OFF_P = OFF_SC + (KF == 1 ? S * SCST : 0);
+  static constexpr int P_BYTES = VB16 ? 16 * PST * 4 : 2 * 4 * 16 * 16;  // f32 [h][token] | fp8 [term][g][h][16]
   static constexpr int OFF_PS = OFF_P + P_BYTES;               // [g][h] e8m0 B scales
   static constexpr int OFF_X = OFF_PS + 64;                    // [4][16] f32 exchange
-  static constexpr int OFF_VOTE = OFF_X + 256;
+  static constexpr int OFF_E = OFF_X + 256;                    // [4] int exchange (V block exponents)
+  static constexpr int OFF_VOTE = OFF_E + 16;
   static constexpr int LDS = OFF_VOTE + 16;
+  static_assert(BLOCKS_PER_CU == 1 || LDS <= 80 * 1024, "two work-groups per CU");
 };
+constexpr int kVScaleSpan = 31;  // fp4 V: P' = P 2^(e - E_ref) <= 2^(96 + 31) stays finite in bf16
+
 
 template <int KF, int VF, bool IDX, bool QB>
 __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_kernel(const DecodeParams p) {
@@ -312,6 +329,7 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
   for (int i = 0; i < 8; ++i) o[i] = v4f{0.f, 0.f, 0.f, 0.f};
   float m_ref = 0.f, m_seen = neg_inf(), l_part = 0.f;
   bool have_ref = false;
+  int e_ref = 127, e_seen = 0;  // fp4 V: reference and running max of the V block exponents
 
   auto prologue = [&](bool slots_issued) {
     if (!slots_issued) {
@@ -354,6 +372,7 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
 
       // ---- scores: rows i = l16 of this wave's slice, 16x16x128 MFMAs ----------
       v4f s = v4f{0.f, 0.f, 0.f, 0.f};
+      int e_w = 0;  // fp4 V: max V block exponent of this wave's 16 tokens
       {
         // all fragment reads first, then the MFMA chain
         const uint8_t* kp = kt + tok_of(w, l16) * C::KST;
@@ -375,6 +394,10 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
           }
 #pragma unroll
           for (int ks = 0; ks < 5; ++ks) s = mfma16_f4f8(ka[ks], ksc[ks], qv[ks], s);
+          if constexpr (C::VB16) {  // V blocks 0..15 are K blocks 4ks + g, ks < 4
+            e_w = wave_max(max(max(ksc[0], ksc[1]), max(ksc[2], ksc[3])));
+            e_seen = max(e_seen, e_w);
+          }
         }
       }
       // s[r] = score(token tok_of(w, 4g + r), head l16)
@@ -389,13 +412,16 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
       mx = fmaxf(mx, shfl_xor_f(mx, 32));
       const float m_w = mx == neg_inf() ? neg_inf() : __builtin_ceilf(mx);
       m_seen = fmaxf(m_seen, m_w);
-      if (!have_ref) {  // first tile of the first pass: m_ref = tile max over the waves
+      int* ex = reinterpret_cast<int*>(smem + C::OFF_E);
+      if (!have_ref) {  // first tile of the first pass: references = tile maxima over the waves
         if (g == 0) xch[16 * w + l16] = m_w;
+        if (C::VB16 && lane == 0) ex[w] = e_w;
         lds_barrier();
         m_ref = fmaxf(fmaxf(xch[l16], xch[16 + l16]), fmaxf(xch[32 + l16], xch[48 + l16]));
+        if constexpr (C::VB16) e_ref = max(max(ex[0], ex[1]), max(ex[2], ex[3]));
         have_ref = true;
       }
-      const bool over = __any(m_w > m_ref + kRebase);
+      const bool over = __any(m_w > m_ref + kRebase) || (C::VB16 && e_w > e_ref + kVScaleSpan);
       if (lane == 0) vote[w] = over ? 1 : 0;
 
       if constexpr (!C::VB16) {
@@ -416,49 +442,17 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
         *reinterpret_cast<uint32_t*>(pl + 4 * 256) = lo;
         if (g == 0) smem[C::OFF_PS + 16 * w + l16] = (uint8_t)min(max((int)dm - 8 + 127, 0), 254);
       } else {
-        // bf16 P = 2^(s - m_ref) at V^T position 4 i + w of token 16 w + i
-        uint16_t* prow = reinterpret_cast<uint16_t*>(smem + C::OFF_P + l16 * C::VTST);
+        // f32 P = 2^(s - m_ref), row-major [head][token]
+        float pw[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const uint32_t pb = f32_to_bf16_bits(__builtin_amdgcn_exp2f(fminf(sv[r] - m_ref, 120.f)));
-          l_part += __uint_as_float(pb << 16);
-          prow[4 * (4 * g + r) + w] = (uint16_t)pb;
+          pw[r] = __builtin_amdgcn_exp2f(fminf(sv[r] - m_ref, 120.f));
+          l_part += pw[r];
         }
-        // fp4 V -> bf16 V^T: thread (tokens di + 16 r, MX block dc); token
-        // di + 16 r lands at position 4 di + r of latent-dim row d
-        const int di = tid & 15, dc = tid >> 4;
-        uint4 raw[4];
-        float scv[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          raw[r] = *reinterpret_cast<const uint4*>(kt + (di + 16 * r) * C::KST + 16 * dc);
-          scv[r] = e8m0_to_f32(sct[256 * dc + 4 * (di + 16 * r)]);
-        }
-        uint8_t* vt = smem + C::OFF_VT;
-#pragma unroll
-        for (int wd = 0; wd < 4; ++wd) {
-          uint32_t bf[4][4];  // [token r][byte bt] -> bf16 pair (dims 2bt, 2bt+1 of the word)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const uint32_t xw = reinterpret_cast<const uint32_t*>(&raw[r])[wd];
-            bf[r][0] = cvt_fp4_byte<0>(xw, scv[r]);
-            bf[r][1] = cvt_fp4_byte<1>(xw, scv[r]);
-            bf[r][2] = cvt_fp4_byte<2>(xw, scv[r]);
-            bf[r][3] = cvt_fp4_byte<3>(xw, scv[r]);
-          }
-#pragma unroll
-          for (int bt = 0; bt < 4; ++bt) {
-            const int d0 = 32 * dc + 8 * wd + 2 * bt;
-            const uint2 ev = make_uint2(__builtin_amdgcn_perm(bf[1][bt], bf[0][bt], 0x05040100u),
-                                        __builtin_amdgcn_perm(bf[3][bt], bf[2][bt], 0x05040100u));
-            const uint2 od = make_uint2(__builtin_amdgcn_perm(bf[1][bt], bf[0][bt], 0x07060302u),
-                                        __builtin_amdgcn_perm(bf[3][bt], bf[2][bt], 0x07060302u));
-            *reinterpret_cast<uint2*>(vt + d0 * C::VTST + 8 * di) = ev;
-            *reinterpret_cast<uint2*>(vt + (d0 + 1) * C::VTST + 8 * di) = od;
-          }
-        }
+        *reinterpret_cast<float4*>(reinterpret_cast<float*>(smem + C::OFF_P) + l16 * C::PST + tok_of(w, 4 * g)) =
+            make_float4(pw[0], pw[1], pw[2], pw[3]);
       }
-      lds_barrier();  // (2) P, its scales, the votes [and V^T] visible
+      lds_barrier();  // (2) P, its scales and the votes visible
       if (__builtin_amdgcn_readfirstlane(*reinterpret_cast<const int*>(vote)) != 0) {
         restart = true;
         break;
@@ -499,16 +493,58 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
           o[dt] = mfma16_f8_bscale(av, pl, bsc, o[dt]);
         }
       } else {
-        const uint8_t* vt = smem + C::OFF_VT + (128 * w + l16) * C::VTST + 16 * g;
-        const uint8_t* pt = smem + C::OFF_P + l16 * C::VTST + 16 * g;
+        // Two 32-token K steps of 16x16x32 bf16 MFMAs per dim tile; lane (m, g)
+        // holds tokens T(g, k) = 8g + k (step 0, k < 8) and 24 + 8g + k (step 1,
+        // k >= 8) in both operands.  V^T: one 4-bit transpose read per 16-dim
+        // tile whose source lane m' reads row T(g, m'), so result lane m gets
+        // dim 16dt + m of those 16 tokens, widened to bf16 at unit scale.
+        // P'^T: P of the same tokens times 2^(e[t, j] - E_ref) for the MX block
+        // j of the tile's dims, in bf16.
+        const float* prow = reinterpret_cast<const float*>(smem + C::OFF_P) + l16 * C::PST;
+        float pv[16];
+        {
+          const float4 p0 = *reinterpret_cast<const float4*>(prow + 8 * g);
+          const float4 p1 = *reinterpret_cast<const float4*>(prow + 8 * g + 4);
+          const float4 p2 = *reinterpret_cast<const float4*>(prow + 32 + 8 * g);
+          const float4 p3 = *reinterpret_cast<const float4*>(prow + 36 + 8 * g);
+          const float pa[16] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w,
+                                p2.x, p2.y, p2.z, p2.w, p3.x, p3.y, p3.z, p3.w};
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const v8bf bq = *reinterpret_cast<const v8bf*>(pt + 64 * j);
-          v8bf av[8];
+          for (int k = 0; k < 16; ++k) pv[k] = pa[k];
+        }
+        const int trow = l16 < 8 ? 8 * g + l16 : 24 + 8 * g + l16;
+        const uint32_t va = lds0 + st * C::STAGE + trow * C::KST + 64 * w;
+        const int* sce = reinterpret_cast<const int*>(sct);
 #pragma unroll
-          for (int dt = 0; dt < 8; ++dt) av[dt] = *reinterpret_cast<const v8bf*>(vt + 16 * dt * C::VTST + 64 * j);
+        for (int jl = 0; jl < 4; ++jl) {
+          const int* se = sce + 64 * (4 * w + jl);  // e8m0 of block 4w + jl (dims 32(4w + jl) ..)
+          const int4 e0 = *reinterpret_cast<const int4*>(se + 8 * g);
+          const int4 e1 = *reinterpret_cast<const int4*>(se + 8 * g + 4);
+          const int4 e2 = *reinterpret_cast<const int4*>(se + 32 + 8 * g);
+          const int4 e3 = *reinterpret_cast<const int4*>(se + 36 + 8 * g);
+          const int ev[16] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w,
+                              e2.x, e2.y, e2.z, e2.w, e3.x, e3.y, e3.z, e3.w};
+          uint32_t bw[8];
 #pragma unroll
-          for (int dt = 0; dt < 8; ++dt) o[dt] = mfma16x32_bf16(av[dt], bq, o[dt]);
+          for (int k = 0; k < 16; k += 2)
+            bw[k / 2] = pack_bf16x2(__builtin_amdgcn_ldexpf(pv[k], ev[k] - e_ref),
+                                    __builtin_amdgcn_ldexpf(pv[k + 1], ev[k + 1] - e_ref));
+          const v8bf b0 = __builtin_bit_cast(v8bf, make_uint4(bw[0], bw[1], bw[2], bw[3]));
+          const v8bf b1 = __builtin_bit_cast(v8bf, make_uint4(bw[4], bw[5], bw[6], bw[7]));
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const int dt = 2 * jl + h;
+            const v2i r = lds_read_tr4(va + 8 * dt);
+            const uint32_t x0 = (uint32_t)r[0], x1 = (uint32_t)r[1];
+            const v8bf a0 = __builtin_bit_cast(
+                v8bf, make_uint4(cvt_fp4_byte<0>(x0, 1.f), cvt_fp4_byte<1>(x0, 1.f), cvt_fp4_byte<2>(x0, 1.f),
+                                 cvt_fp4_byte<3>(x0, 1.f)));
+            const v8bf a1 = __builtin_bit_cast(
+                v8bf, make_uint4(cvt_fp4_byte<0>(x1, 1.f), cvt_fp4_byte<1>(x1, 1.f), cvt_fp4_byte<2>(x1, 1.f),
+                                 cvt_fp4_byte<3>(x1, 1.f)));
+            o[dt] = mfma16x32_bf16(a0, b0, o[dt]);
+            o[dt] = mfma16x32_bf16(a1, b1, o[dt]);
+          }
         }
       }
     }
@@ -516,8 +552,13 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
     // drain the ring (the prologue reuses it); m_ref = running max over the waves
     wait_vmcnt<0>();
     if (g == 0) xch[16 * w + l16] = m_seen;
+    if (C::VB16 && lane == 0) reinterpret_cast<int*>(smem + C::OFF_E)[w] = e_seen;
     lds_barrier();
     m_ref = fmaxf(fmaxf(xch[l16], xch[16 + l16]), fmaxf(xch[32 + l16], xch[48 + l16]));
+    if constexpr (C::VB16) {
+      const int* ex = reinterpret_cast<const int*>(smem + C::OFF_E);
+      e_ref = max(max(ex[0], ex[1]), max(ex[2], ex[3]));
+    }
 #pragma unroll
     for (int i = 0; i < 8; ++i) o[i] = v4f{0.f, 0.f, 0.f, 0.f};
     l_part = 0.f;
@@ -531,7 +572,8 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
   if (g == 0) xch[16 * w + l16] = l;
   lds_barrier();
   const float L = xch[l16] + xch[16 + l16] + xch[32 + l16] + xch[48 + l16];
-  const float inv = L > 0.f ? vscale / L : 0.f;
+  const float vs = C::VB16 ? e8m0_to_f32((uint32_t)e_ref) : vscale;  // fp4 V: 2^(E_ref - 127)
+  const float inv = L > 0.f ? vs / L : 0.f;
   const int head = l16;
   if (slot < 0) {
     if (p.lse_out != nullptr && w == 0 && g == 0)

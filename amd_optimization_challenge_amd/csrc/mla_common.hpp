@@ -260,6 +260,13 @@ __device__ __forceinline__ v2i lds_read_tr8(uint32_t lds_off) {
   typedef __attribute__((address_space(3))) v2i lds_v2i;
   return __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(uintptr_t)lds_off);
 }
+// ds_read_b64_tr_b4: within each 16-lane group, result lane j gets nibble j of
+// the 8-byte read of lane m as its nibble m, m = 0..15 (a 16 x 16 nibble
+// transpose)
+__device__ __forceinline__ v2i lds_read_tr4(uint32_t lds_off) {
+  typedef __attribute__((address_space(3))) v2i lds_v2i;
+  return __builtin_amdgcn_ds_read_tr4_b64_v2i32((lds_v2i*)(uintptr_t)lds_off);
+}
 
 // Byte-transpose of a 4x4 byte block: y[e] byte r = x[r] byte e.
 __device__ __forceinline__ void transpose4x4_bytes(uint32_t x0, uint32_t x1, uint32_t x2,

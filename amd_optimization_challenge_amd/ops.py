@@ -282,11 +282,11 @@ def _a256(x: int) -> int:
 
 
 def blocks_per_cu(num_heads: int, kv_mode: int) -> int:
-    """Resident decode work-groups per CU: 2 for H = 16 with the fp8 cache (two-stage
-    ring), else 1; kv_mode < 0 gives the largest over the modes."""
+    """Resident decode work-groups per CU: 2 for H = 16 with one cache (fp8 or
+    mxfp4), else 1; kv_mode < 0 gives the largest over the modes."""
     if num_heads != 16:
         return 1
-    return 2 if kv_mode <= 0 else 1
+    return 2 if kv_mode <= 1 else 1
 
 
 def target_items(batch: int, num_heads: int, kv_mode: int, num_cu: int) -> int:
