@@ -137,7 +137,11 @@ struct H16 {
   // (two caches) runs one work-group per CU.
   static constexpr int S = KF == 0 ? 2 : (VF == 1 ? 2 : 3);
   static constexpr int BLOCKS_PER_CU = VF == 1 ? 1 : 2;
-  static constexpr int RW0 = KF == 1 ? 1 : 0;                  // waves RW0..3 DMA rows; wave 0 the scales
+  // DMA issue: waves RW0..3 gather rows.  fp4 K + fp8 V: wave 0 gathers the
+  // 18 scale bytes of every token (SCW = 1); fp4 K = V: every wave gathers rows
+  // and scale byte columns j = w + 4k (SCW = 4), so no wave issues a long burst
+  static constexpr int RW0 = (KF == 1 && VF == 1) ? 1 : 0;
+  static constexpr int SCW = KF == 0 ? 0 : (VF == 1 ? 1 : 4);
   static constexpr int NRW = 4 - RW0;
   static constexpr int NA = (NW + NRW - 1) / NRW;              // windows per row wave: NA or NA - 1
   static constexpr int NAW = NW % NRW == 0 ? NRW : NW % NRW;   // row waves (from RW0) that issue NA
@@ -220,28 +224,40 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
       else if (u < C::NW) dma16_to_lds(p.v_cache + (int64_t)sl[k] * p.v_row_stride + co[k], sbase + 1024 * u);
     }
   };
-  // fp4 K scales: wave 0 DMAs the 18 e8m0 bytes of token `lane` of tile t, one
-  // byte per lane and instruction; byte j lands in dword j * 64 + lane of the
-  // tile's scale stage (sub-dword LDS-DMA writes one dword per lane)
+  // fp4 K scales: the e8m0 bytes of token `lane` of tile t, one byte per lane
+  // and instruction; byte j lands in dword j * 64 + lane of the tile's scale
+  // stage (sub-dword LDS-DMA writes one dword per lane).  Byte columns j = w +
+  // SCW k are this wave's.
   auto issue_scales = [&](int t) {
     if constexpr (KF == 1) {
-      if (w == 0) {
+      if (w < C::SCW) {
         const uint8_t* srow = p.k_scales + (int64_t)slot_of(t, lane) * p.k_scale_stride;
         const uint32_t sb = lds0 + C::OFF_SC + (t % C::S) * C::SCST;
 #pragma unroll
-        for (int j = 0; j < kMxBlocks; ++j) dma1_to_lds(srow + j, sb + 256 * j);
+        for (int k = 0; k < (kMxBlocks + C::SCW - 1) / C::SCW; ++k) {
+          const int j = w + C::SCW * k;
+          if (j < kMxBlocks) dma1_to_lds(srow + j, sb + 256 * j);
+        }
       }
     }
   };
   // this wave's wait for tile t's rows (and scales), k groups issued after them
   auto wait_tile = [&](int k) {
-    if constexpr (KF == 1) {
-      constexpr int SL = IDX ? 1 : 0;  // wave 0: one slot DMA + 18 scale DMAs per group
+    constexpr int SL = IDX ? 1 : 0;  // wave 0 issues one slot DMA per group
+    if constexpr (KF == 1 && C::SCW == 4) {
+      // rows: NA for waves < NAW, else NA - 1; scale columns: 5 for waves 0, 1, else 4
+      constexpr int SC0 = (kMxBlocks + 3) / 4, SC1 = kMxBlocks / 4, R = kMxBlocks % 4;
+      static_assert(C::RW0 == 0 && C::NAW == 3 && R == 2, "per-wave DMA counts");
+      if (w == 0) wait_groups<C::NA + SC0 + SL>(k);
+      else if (w == 1) wait_groups<C::NA + SC0>(k);
+      else if (w == 2) wait_groups<C::NA + SC1>(k);
+      else wait_groups<C::NA - 1 + SC1>(k);
+    } else if constexpr (KF == 1) {
+      // wave 0: one slot DMA + 18 scale DMAs per group
       if (w == 0) wait_groups<kMxBlocks + SL>(k);
       else if (w - C::RW0 < C::NAW) wait_groups<C::NA>(k);
       else wait_groups<C::NA - 1>(k);
     } else {
-      constexpr int SL = IDX ? 1 : 0;  // wave 0 issues one slot DMA per group
       if (w == 0) wait_groups<C::NA + SL>(k);
       else if (w < C::NAW) wait_groups<C::NA>(k);
       else wait_groups<C::NA - 1>(k);
@@ -512,6 +528,8 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
 #pragma unroll
           for (int k = 0; k < 16; ++k) pv[k] = pa[k];
         }
+#pragma unroll
+        for (int k = 0; k < 16; ++k) pv[k] = __builtin_amdgcn_ldexpf(pv[k], -e_ref);  // 2^(e - E_ref) below
         const int trow = l16 < 8 ? 8 * g + l16 : 24 + 8 * g + l16;
         const uint32_t va = lds0 + st * C::STAGE + trow * C::KST + 64 * w;
         const int* sce = reinterpret_cast<const int*>(sct);
@@ -527,8 +545,7 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
           uint32_t bw[8];
 #pragma unroll
           for (int k = 0; k < 16; k += 2)
-            bw[k / 2] = pack_bf16x2(__builtin_amdgcn_ldexpf(pv[k], ev[k] - e_ref),
-                                    __builtin_amdgcn_ldexpf(pv[k + 1], ev[k + 1] - e_ref));
+            bw[k / 2] = pack_bf16x2(__builtin_amdgcn_ldexpf(pv[k], ev[k]), __builtin_amdgcn_ldexpf(pv[k + 1], ev[k + 1]));
           const v8bf b0 = __builtin_bit_cast(v8bf, make_uint4(bw[0], bw[1], bw[2], bw[3]));
           const v8bf b1 = __builtin_bit_cast(v8bf, make_uint4(bw[4], bw[5], bw[6], bw[7]));
 #pragma unroll

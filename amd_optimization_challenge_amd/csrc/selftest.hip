@@ -211,6 +211,7 @@ __device__ __forceinline__ void dma2_to_lds(const void* g, uint32_t lds_off) {
 //     131072+4096; out = the three 1 KiB LDS windows.
 // 14: LDS[i] = in[i % 1024] for i < 4096; lane l tr-reads at 8l (pattern A) and
 //     at 64(l % 8) + 8(l / 8) (pattern B); out = 64 x 8 bytes per pattern.
+// 21: as 14 with ds_read_b64_tr_b4.
 __global__ void lds_probe_kernel(int which, const uint8_t* __restrict__ src, uint8_t* __restrict__ out) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[136192];
   const int l = threadIdx.x;
@@ -235,15 +236,16 @@ __global__ void lds_probe_kernel(int which, const uint8_t* __restrict__ src, uin
   } else {
     for (int i = l; i < 4096; i += 64) lds[i] = src[i % 1024];
     __syncthreads();
-    const v2i a = lds_read_tr8(base + 8 * l);
-    const v2i b = lds_read_tr8(base + 64 * (l % 8) + 8 * (l / 8));
+    const v2i a = which == 21 ? lds_read_tr4(base + 8 * l) : lds_read_tr8(base + 8 * l);
+    const v2i b = which == 21 ? lds_read_tr4(base + 64 * (l % 8) + 8 * (l / 8))
+                              : lds_read_tr8(base + 64 * (l % 8) + 8 * (l / 8));
     reinterpret_cast<v2i*>(out)[l] = a;
     reinterpret_cast<v2i*>(out)[64 + l] = b;
   }
 }
 
 hipError_t launch_selftest(int which, const void* in, void* out, hipStream_t stream) {
-  if (which == 13 || which == 14 || which == 17 || which == 18) {
+  if (which == 13 || which == 14 || which == 17 || which == 18 || which == 21) {
     hipLaunchKernelGGL(lds_probe_kernel, dim3(1), dim3(64), 0, stream, which,
                        static_cast<const uint8_t*>(in), static_cast<uint8_t*>(out));
     return hipGetLastError();

@@ -12,7 +12,7 @@ pytestmark = pytest.mark.gpu
 
 IN_BYTES = {0: 4096, 1: 4096, 2: 3136, 3: 3136, 4: 1024, 5: 2048, 6: 1024, 7: 512, 8: 1024, 9: 1024,
             10: 256, 11: 0, 12: 0, 13: 1024, 14: 1024, 15: 4160, 16: 4160, 17: 1024, 18: 1024, 19: 4160,
-            20: 16388}
+            20: 16388, 21: 1024}
 
 
 def run(which, inp: np.ndarray, out_bytes: int) -> np.ndarray:
@@ -226,6 +226,24 @@ def test_lds_transpose_read_b8(cuda):
             g, j = l // 16, l % 16
             for m in range(8):
                 exp[l, m] = rows[16 * g + 2 * m + (j >> 3), j & 7]
+        assert np.array_equal(got[pat], exp), pat
+
+
+def test_lds_transpose_read_b4(cuda):
+    """ds_read_b64_tr_b4: lane j of each 16-lane group gets nibble j of lane m's
+    8-byte read as its nibble m (a 16 x 16 nibble transpose); the mxfp4 decode
+    reads its V^T fragments this way."""
+    src = np.random.default_rng(15).integers(0, 256, 1024, dtype=np.uint8)
+    lds = np.resize(src, 4096)
+    got = run(21, src, 2 * 64 * 8).reshape(2, 64, 8)
+    nib = lambda row, k: (row[k >> 1] >> (4 * (k & 1))) & 15
+    for pat, addr in enumerate([8 * np.arange(64), 64 * (np.arange(64) % 8) + 8 * (np.arange(64) // 8)]):
+        rows = np.stack([lds[a:a + 8] for a in addr])
+        exp = np.zeros((64, 8), np.uint8)
+        for l in range(64):
+            g, j = l // 16, l % 16
+            for m in range(16):
+                exp[l, m >> 1] |= np.uint8(nib(rows[16 * g + m], j) << (4 * (m & 1)))
         assert np.array_equal(got[pat], exp), pat
 
 
