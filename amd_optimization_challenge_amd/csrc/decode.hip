@@ -515,7 +515,9 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
         // tile whose source lane m' reads row T(g, m'), so result lane m gets
         // dim 16dt + m of those 16 tokens, widened to bf16 at unit scale.
         // P'^T: P of the same tokens times 2^(e[t, j] - E_ref) for the MX block
-        // j of the tile's dims, in bf16.
+        // j of the tile's dims, in bf16.  The shift is applied in one step: a
+        // small P whose token has a large block exponent would lose its mantissa
+        // to f32 subnormals if P were scaled by 2^-E_ref first.
         const float* prow = reinterpret_cast<const float*>(smem + C::OFF_P) + l16 * C::PST;
         float pv[16];
         {
@@ -528,8 +530,6 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
 #pragma unroll
           for (int k = 0; k < 16; ++k) pv[k] = pa[k];
         }
-#pragma unroll
-        for (int k = 0; k < 16; ++k) pv[k] = __builtin_amdgcn_ldexpf(pv[k], -e_ref);  // 2^(e - E_ref) below
         const int trow = l16 < 8 ? 8 * g + l16 : 24 + 8 * g + l16;
         const uint32_t va = lds0 + st * C::STAGE + trow * C::KST + 64 * w;
         const int* sce = reinterpret_cast<const int*>(sct);
@@ -545,7 +545,8 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
           uint32_t bw[8];
 #pragma unroll
           for (int k = 0; k < 16; k += 2)
-            bw[k / 2] = pack_bf16x2(__builtin_amdgcn_ldexpf(pv[k], ev[k]), __builtin_amdgcn_ldexpf(pv[k + 1], ev[k + 1]));
+            bw[k / 2] = pack_bf16x2(__builtin_amdgcn_ldexpf(pv[k], ev[k] - e_ref),
+                                    __builtin_amdgcn_ldexpf(pv[k + 1], ev[k + 1] - e_ref));
           const v8bf b0 = __builtin_bit_cast(v8bf, make_uint4(bw[0], bw[1], bw[2], bw[3]));
           const v8bf b1 = __builtin_bit_cast(v8bf, make_uint4(bw[4], bw[5], bw[6], bw[7]));
 #pragma unroll

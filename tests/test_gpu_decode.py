@@ -66,6 +66,37 @@ def test_wide_score_range(cuda, heads, mode):
     assert_close(got, ref)
 
 
+@pytest.mark.parametrize("growth", [20, 45, 90])
+def test_mxfp4_value_scale_growth(cuda, growth):
+    """fp4 V (H = 16): the per-token MX block scales are folded into P relative
+    to a per-item reference exponent.  Latent values that grow by 2^growth
+    over the sequence push later block exponents above it (45 and 90 exceed
+    the span a bf16 P' can carry, so the item restarts from a higher
+    reference); Q is zero on dims 0..511, so the scores stay ordinary while V
+    (and K's first 512 dims) change scale."""
+    print(f"mxfp4 V scale growth 2^{growth}", flush=True)
+    g = torch.Generator().manual_seed(23)
+    lens = [700, 129, 64]
+    T = sum(lens)
+    q = torch.randn(len(lens), 16, 576, generator=g)
+    q[..., :512] = 0.0
+    kv = torch.randn(T, 1, 576, generator=g)
+    pos = torch.cat([torch.arange(L) for L in lens]).float()
+    grow = torch.exp2(growth * pos / 700.0)
+    kv[:, 0, :512] *= grow[:, None]
+    indptr = torch.tensor([0] + list(np.cumsum(lens)), dtype=torch.int32)
+    idx = torch.randperm(T, generator=g).to(torch.int32)
+    rows = torch.empty_like(kv)
+    rows[idx.long()] = kv
+    case = case_from_tensors(q.to(torch.bfloat16), rows.to(torch.bfloat16), indptr, idx, "mxfp4")
+    got, ref, _ = run_case(case, "mxfp4", 1 / math.sqrt(192))
+    assert np.all(np.isfinite(got))
+    # compare relative to each row's own magnitude (the outputs span 2^growth)
+    for b in range(len(lens)):
+        s = float(np.abs(ref[b]).max()) or 1.0
+        assert_close(got[b] / s, ref[b] / s)
+
+
 @pytest.mark.parametrize("heads,mode", [(16, "fp8"), (128, "fp8"), (16, "mxfp4")])
 def test_cache_permutation_is_exact(cuda, heads, mode):
     # moving cache rows together with kv_indices leaves the output bit-identical
