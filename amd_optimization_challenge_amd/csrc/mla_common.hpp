@@ -210,6 +210,15 @@ __device__ __forceinline__ void dma4_to_lds(const void* g, uint32_t lds_off) {
                : "s"(__builtin_amdgcn_readfirstlane(lds_off)), "v"(g)
                : "memory");
 }
+// two bytes per lane (2-byte aligned source): lane l's bytes land,
+// zero-extended, in the dword at M0 + 4 l
+__device__ __forceinline__ void dma2_to_lds(const void* g, uint32_t lds_off) {
+  uint32_t tmp;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tglobal_load_lds_ushort %2, off\n\ts_mov_b32 m0, %0"
+               : "=&s"(tmp)
+               : "s"(__builtin_amdgcn_readfirstlane(lds_off)), "v"(g)
+               : "memory");
+}
 // one byte per lane: lane l's byte lands, zero-extended, in the dword at M0 + 4 l
 __device__ __forceinline__ void dma1_to_lds(const void* g, uint32_t lds_off) {
   uint32_t tmp;

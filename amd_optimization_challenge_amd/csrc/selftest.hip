@@ -200,12 +200,6 @@ __global__ void fp4_probe_kernel(int big, float* __restrict__ out) {
   }
 }
 
-// sub-dword LDS-DMA (probe 17; dma1_to_lds is the product's ubyte form)
-__device__ __forceinline__ void dma2_to_lds(const void* g, uint32_t lds_off) {
-  uint32_t tmp;
-  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tglobal_load_lds_ushort %2, off\n\ts_mov_b32 m0, %0"
-               : "=&s"(tmp) : "s"(lds_off), "v"(g) : "memory");
-}
 // LDS-DMA placement (13) and ds_read_b64_tr_b8 (14).  in: 1024 source bytes.
 // 13: lane l DMAs src[16*((7l) % 64) ..+16] to LDS offsets 0, 65536+1024 and
 //     131072+4096; out = the three 1 KiB LDS windows.

@@ -97,6 +97,30 @@ def test_mxfp4_value_scale_growth(cuda, growth):
         assert_close(got[b] / s, ref[b] / s)
 
 
+@pytest.mark.parametrize("heads,mode", [(16, "mxfp4"), (16, "mxfp4k_fp8v"), (128, "mxfp4k_fp8v")])
+def test_mxfp4_scale_row_stride(cuda, heads, mode):
+    """The e8m0 scale rows may be padded (stride > 18, odd or even); every
+    stride gives the stride-18 result bit for bit."""
+    print(f"scale stride H={heads} mode={mode}", flush=True)
+    case = host_case([700, 129, 64, 1], heads, mode, seed=29, permute=True)
+    q, kv, indptr, idx, qb, caches = case
+    data = device_data(q, kv, indptr, idx, caches, mode, 1 / math.sqrt(192))
+    from oracle import mla_oracle as O
+
+    base = custom_kernel(data).clone()
+    torch.cuda.synchronize()
+    _, ref = O.reference_path(qb, mode, caches, indptr.numpy(), idx.numpy(), 1 / math.sqrt(192))
+    assert_close(base.float().cpu().numpy(), ref)
+    packed, sc = data[1]["mxfp4"]
+    for cols in (19, 24, 25):
+        wide = torch.full((sc.shape[0], cols), 127, dtype=torch.uint8, device=sc.device)
+        wide[:, :18] = sc.view(torch.uint8)
+        data[1]["mxfp4"] = (packed, wide.view(torch.float8_e8m0fnu))
+        got = custom_kernel(data)
+        torch.cuda.synchronize()
+        assert torch.equal(got, base), cols
+
+
 @pytest.mark.parametrize("heads,mode", [(16, "fp8"), (128, "fp8"), (16, "mxfp4")])
 def test_cache_permutation_is_exact(cuda, heads, mode):
     # moving cache rows together with kv_indices leaves the output bit-identical
