@@ -622,33 +622,33 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
 // work item and all 512 latent dims, so the softmax state and O^T never leave
 // the wave.  Q^T (the QK B operand) stays in registers, O^T in accumulators.
 // Cache rows are gathered straight into an LDS ring by LDS-DMA (no staging
-// registers), S tiles deep; the PV A operand (V^T) is read from the row-major
-// tile with ds_read_b64_tr_b8, so no transposed copy is ever written.
-//   KF: 0 = fp8 K rows, V = same rows; 1 = fp4 K rows + e8m0, V = fp8 cache
+// registers), two tiles deep; the PV A operand (V^T) is read from the row-major
+// tile with ds_read_b64_tr_b8, so no transposed copy is ever written.  This
+// kernel serves the two-cache mode: fp4 K rows + e8m0 scales for QK, the fp8
+// cache's rows for V (the fp8-only mode runs decode_h128p_kernel below).
 // Online softmax is rescaled lazily: the exponent base m only moves when a
 // head's tile max exceeds it by more than 8 (log2 units), so P <= 2^8 fits
 // e4m3 and O^T is touched by VALU only on those (rare) tiles.
 // ============================================================================
-template <int KF>
 struct H128 {
   static constexpr int NT = 256;
-  static constexpr int KST = KF == 0 ? 592 : 304;              // K row stride in LDS
-  static constexpr int KCH = KF == 0 ? 36 : 18;                // real 16-B chunks per K row
-  static constexpr int VST = 528;                              // fp8 V row stride (KF == 1)
-  static constexpr int KDMA = (kTile * KST + 1023) / 1024;     // 1-KiB DMA windows: 37 / 19
-  static constexpr int VDMA = KF == 1 ? (kTile * VST + 1023) / 1024 : 0;  // 33
-  static constexpr int DPW = (KDMA + VDMA + 3) / 4;            // windows per wave: 10 / 13
+  static constexpr int KST = 304;                              // fp4 K row stride in LDS
+  static constexpr int KCH = 18;                               // real 16-B chunks per K row
+  static constexpr int VST = 528;                              // fp8 V row stride
+  static constexpr int KDMA = (kTile * KST + 1023) / 1024;     // 1-KiB DMA windows: 19
+  static constexpr int VDMA = (kTile * VST + 1023) / 1024;     // 33
+  static constexpr int DPW = (KDMA + VDMA + 3) / 4;            // windows per wave: 13
   static constexpr int STAGE = 4 * DPW * 1024;                 // ring stage bytes
-  static constexpr int S = KF == 0 ? 3 : 2;                    // ring depth (tiles)
-  static constexpr int OFF_V = KDMA * 1024;                    // V rows inside a stage (KF == 1)
+  static constexpr int S = 2;                                  // ring depth (tiles)
+  static constexpr int OFF_V = KDMA * 1024;                    // V rows inside a stage
   static constexpr int OFF_SLOT = S * STAGE;                   // [S][64] int32 cache slots
   static constexpr int OFF_VOTE = OFF_SLOT + S * 256;          // [2][4] restart votes
   static constexpr int LDS = OFF_VOTE + 16;
 };
 
-template <int KF, bool IDX>
+template <bool IDX>
 __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams p) {
-  using C = H128<KF>;
+  using C = H128;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[C::LDS];
   const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
 
@@ -664,14 +664,14 @@ __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams 
   const int lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
   const int head = 32 * w + l32;
 
-  // ---- Q^T B operand, K-step ks = dims 64ks .. +63 (fp4 K: partner order) -----
+  // ---- Q^T B operand, K-step ks = dims 64ks .. +63 (fp4 K partner order) -----
   v8i qv[9];
   {
     const uint8_t* qrow = p.q_fp8 + ((int64_t)b * 128 + head) * kQKDim;
 #pragma unroll
     for (int ks = 0; ks < 9; ++ks) {
-      const int d0 = KF == 0 ? 64 * ks + 32 * hh : 64 * ks + 16 * hh;
-      const int d1 = KF == 0 ? d0 + 16 : d0 + 32;
+      const int d0 = 64 * ks + 16 * hh;
+      const int d1 = d0 + 32;
       const uint4 lo = *reinterpret_cast<const uint4*>(qrow + d0);
       const uint4 hi = *reinterpret_cast<const uint4*>(qrow + d1);
       qv[ks] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
@@ -681,7 +681,7 @@ __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams 
   }
   const float qs = p.q_scale[0];
   const float kvs = p.kv_scale[0];
-  const float c = qs * (KF == 0 ? kvs : 1.0f) * p.sm_scale * kLog2e;
+  const float c = qs * p.sm_scale * kLog2e;  // K's scales ride on the MFMA's A scale
   const float vscale = kvs;  // the 2^8 carried by P' is folded into the PV scale exponent
 
   v16f o[16];
@@ -717,7 +717,7 @@ __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams 
         if (tok >= kTile) { tok = kTile - 1; pos = 0; }
         sl[k] = slot_of(st, tok, pos0);
         co[k] = 16 * min(pos, C::KCH - 1);
-      } else if (KF == 1 && u < C::KDMA + C::VDMA) {
+      } else if (u < C::KDMA + C::VDMA) {
         const int bb = 1024 * (u - C::KDMA) + 16 * lane;
         int tok = bb / C::VST, pos = (bb - tok * C::VST) >> 4;
         if (tok >= kTile) { tok = kTile - 1; pos = 0; }
@@ -731,7 +731,7 @@ __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams 
 #pragma unroll
     for (int k = 0; k < C::DPW; ++k) {
       const int u = w + 4 * k;
-      const bool vrow = KF == 1 && u >= C::KDMA && u < C::KDMA + C::VDMA;
+      const bool vrow = u >= C::KDMA && u < C::KDMA + C::VDMA;
       const uint8_t* src = vrow ? p.v_cache + (int64_t)sl[k] * p.v_row_stride + co[k]
                                 : p.k_cache + (int64_t)sl[k] * p.k_row_stride + co[k];
       dma16_to_lds(src, sbase + 1024 * u);
@@ -740,40 +740,29 @@ __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams 
   // fp4 K scales: lane (token u*32 + l32) needs blocks 2ks + hh, ks = 0..8
   uint32_t sc_nxt[2][9], sc_cur[2][9];
   auto load_scales = [&](int t) {
-    if constexpr (KF == 1) {
-      const int st = t % C::S;
-      const int pos0 = t_beg + kTile * t;
+    const int st = t % C::S;
+    const int pos0 = t_beg + kTile * t;
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const uint8_t* srow = p.k_scales + (int64_t)slot_of(st, 32 * u + l32, pos0) * p.k_scale_stride;
+    for (int u = 0; u < 2; ++u) {
+      const uint8_t* srow = p.k_scales + (int64_t)slot_of(st, 32 * u + l32, pos0) * p.k_scale_stride;
 #pragma unroll
-        for (int ks = 0; ks < 9; ++ks) sc_nxt[u][ks] = srow[2 * ks + hh];
-      }
+      for (int ks = 0; ks < 9; ++ks) sc_nxt[u][ks] = srow[2 * ks + hh];
     }
   };
 
   auto prologue = [&]() {
-    // prologue: slots(0) visible; rows(0) [+ scales(0)] in flight; slots(1), and for S = 3
-    // rows(1) and slots(2), issued in the order the steady-state waits assume
+    // slots(0) visible; then rows(0) + scales(0) and slots(1) in flight
     issue_slots(0);
     wait_vmcnt<0>();
     lds_barrier();
     issue_slots(1);
     issue_rows(0);
     load_scales(0);
-    if constexpr (C::S == 3) {
-      if (ntiles > 1) {
-        wait_vmcnt<C::DPW>();  // slots(1) landed (rows(0) may still be in flight)
-        lds_barrier();
-        issue_slots(2);
-        issue_rows(1);
-      }
-    }
   };
 
   // lane-constant parts of the transpose-read addresses (PV A operand)
-  const int vrow_st = KF == 0 ? C::KST : C::VST;
-  const int voff = KF == 0 ? 0 : C::OFF_V;
+  const int vrow_st = C::VST;
+  const int voff = C::OFF_V;
   int tr_off[4];
   {
     const int G = lane >> 4, m = (lane & 15) >> 1, oo = lane & 1;
@@ -800,19 +789,12 @@ __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams 
   for (int ti = 0; ti < ntiles; ++ti) {
     const int st = ti % C::S;
     const int nval = min(kTile, ntok - kTile * ti);
-    // tile ti landed (and slots for the tile issued next); see the prologue order
-    if constexpr (C::S == 3) {
-      if (ti + 1 < ntiles) wait_vmcnt<C::DPW>();
-      else wait_vmcnt<0>();
-    } else {
-      wait_vmcnt<0>();
-    }
-    if constexpr (KF == 1) {
+    // tile ti and its scales landed (and the slots of the tile issued next)
+    wait_vmcnt<0>();
 #pragma unroll
-      for (int u = 0; u < 2; ++u)
+    for (int u = 0; u < 2; ++u)
 #pragma unroll
-        for (int ks = 0; ks < 9; ++ks) sc_cur[u][ks] = sc_nxt[u][ks];
-    }
+      for (int ks = 0; ks < 9; ++ks) sc_cur[u][ks] = sc_nxt[u][ks];
     lds_barrier();  // tile ti visible; the stage of tile ti-1 is free
     if (ti > 0 && __builtin_amdgcn_readfirstlane(*reinterpret_cast<const uint32_t*>(vote + 4 * ((ti - 1) & 1))) != 0) {
       restart = true;
@@ -821,18 +803,16 @@ __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams 
     if (ti + C::S - 1 < ntiles) {
       issue_slots(ti + C::S);
       issue_rows(ti + C::S - 1);
-      if constexpr (KF == 1) load_scales(ti + C::S - 1);
+      load_scales(ti + C::S - 1);
     }
 
     // ---- scores S^T: s0 = tokens 0..31, s1 = tokens 32..63 of the tile ------------
-    const uint32_t sb = lds0 + st * C::STAGE;
     const uint8_t* kt = smem + st * C::STAGE;
     v16f s0 = v16f{}, s1 = v16f{};
     // one K-step of lookahead on the LDS fragments; sched_barrier keeps the
     // compiler from hoisting every fragment load (register blow-up)
     auto kfrag = [&](int ks, int u) -> v8i {
-      if constexpr (KF == 0) return ld_v8(kt + (32 * u + l32) * C::KST + 64 * ks + 32 * hh);
-      else return ld_v4_as_v8(kt + (32 * u + l32) * C::KST + 16 * (2 * ks + hh));
+      return ld_v4_as_v8(kt + (32 * u + l32) * C::KST + 16 * (2 * ks + hh));
     };
     v8i a0n = kfrag(0, 0), a1n = kfrag(0, 1);
 #pragma unroll
@@ -842,16 +822,10 @@ __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams 
         a0n = kfrag(ks + 1, 0);
         a1n = kfrag(ks + 1, 1);
       }
-      if constexpr (KF == 0) {
-        s0 = mfma32_f8(a0, qv[ks], s0);
-        s1 = mfma32_f8(a1, qv[ks], s1);
-      } else {
-        s0 = mfma32_f4f8(a0, (int)sc_cur[0][ks], qv[ks], s0);
-        s1 = mfma32_f4f8(a1, (int)sc_cur[1][ks], qv[ks], s1);
-      }
+      s0 = mfma32_f4f8(a0, (int)sc_cur[0][ks], qv[ks], s0);
+      s1 = mfma32_f4f8(a1, (int)sc_cur[1][ks], qv[ks], s1);
       __builtin_amdgcn_sched_barrier(0);
     }
-    (void)sb;
     // s_u[r] = raw score(token 32u + 8(r/4) + 4hh + r%4, head); masked on a partial tile
     if (nval < kTile) {
 #pragma unroll
@@ -1450,7 +1424,7 @@ static hipError_t launch_decode_t(const DecodeParams& p, int kv_mode, int grid, 
     if (QB) return hipErrorInvalidValue;  // the H = 128 kernel takes a quantized Q
     switch (kv_mode) {
       case 0: hipLaunchKernelGGL((decode_h128p_kernel<IDX>), dim3(grid), dim3(256), 0, stream, p); break;
-      case 2: hipLaunchKernelGGL((decode_h128_kernel<1, IDX>), dim3(grid), dim3(256), 0, stream, p); break;
+      case 2: hipLaunchKernelGGL((decode_h128_kernel<IDX>), dim3(grid), dim3(256), 0, stream, p); break;
       default: return hipErrorInvalidValue;
     }
   } else {
