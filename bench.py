@@ -248,6 +248,45 @@ def bench_append(n_tokens, steps, warmup):
             "bytes_per_launch": nbytes, "achieved_GBs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
 
 
+def bench_neighbours(steps, warmup):
+    """W_UK absorption and v_up_proj (+ per-tensor FP8) at the H = 128 (config 3,
+    B = 64) and H = 16 (config 2, B = 32) shapes: mean device time per call and
+    the HBM rate of algorithmic bytes (weights + activations read, result
+    written; the products are weight-streaming GEMMs)."""
+    import torch
+
+    from amd_optimization_challenge_amd import neighbours as N
+
+    out = []
+    for B, H in [(64, 128), (32, 16)]:
+        g = torch.Generator().manual_seed(B + H)
+        qn = torch.randn((B, H, 128), generator=g).to(torch.bfloat16).cuda()
+        qr = torch.randn((B, H, 64), generator=g).to(torch.bfloat16).cuda()
+        w_uk = (torch.randn((H, 128, 512), generator=g) / 11.3).to(torch.bfloat16).cuda()
+        o = torch.randn((B, H, 512), generator=g).to(torch.bfloat16).cuda()
+        w_uv = (torch.randn((H, 512, 128), generator=g) / 22.6).to(torch.bfloat16).cuda()
+        cases = [("absorb_q", lambda: N.absorb_q(qn, qr, w_uk), 2 * (H * 128 * 512 + B * H * 192 + B * H * 576)),
+                 ("v_up_proj", lambda: N.v_up_proj(o, w_uv), 2 * (H * 512 * 128 + B * H * 512 + B * H * 128)),
+                 ("v_up_proj+fp8", lambda: N.v_up_proj(o, w_uv, quant_fp8=True),
+                  2 * (H * 512 * 128 + B * H * 512) + B * H * 128)]
+        for name, fn, nbytes in cases:
+            for _ in range(warmup):
+                fn()
+            torch.cuda.synchronize()
+            ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+            ev[0].record()
+            for _ in range(steps):
+                fn()
+            ev[1].record()
+            torch.cuda.synchronize()
+            us = ev[0].elapsed_time(ev[1]) * 1e3 / steps
+            gbs = nbytes / (us * 1e-6) / 1e9
+            out.append({"op": name, "batch": B, "num_heads": H, "us_per_call": round(us, 3),
+                        "bytes_alg": nbytes, "achieved_GBs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)})
+    return {"metric": "neighbouring steps (W_UK absorption, v_up_proj), us per call", "steps": steps,
+            "warmup": warmup, "results": out}
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -259,6 +298,8 @@ def main(argv=None):
     ap.add_argument("--cpu-budget-s", type=float, default=10.0)
     ap.add_argument("--append-tokens", type=int, default=0,
                     help="time the KV-cache append writer at this many tokens instead (own JSON line)")
+    ap.add_argument("--neighbours", action="store_true",
+                    help="time W_UK absorption and v_up_proj (+fp8) instead (own JSON line)")
     ap.add_argument("--profile-decode", action="store_true",
                     help="decode-only launches for counter collection (no JSON line)")
     args = ap.parse_args(argv)
@@ -273,6 +314,9 @@ def main(argv=None):
     _lib.load()
     if args.append_tokens > 0:
         print(json.dumps(bench_append(args.append_tokens, args.steps, args.warmup)), flush=True)
+        return 0
+    if args.neighbours:
+        print(json.dumps(bench_neighbours(args.steps, args.warmup)), flush=True)
         return 0
     if args.profile_decode:
         profile_decode([args.config] if args.only_headline else sorted(inputs.CONFIGS), max(1, args.steps))

@@ -27,6 +27,10 @@ task files):
 * ``mla_decode``               -- the dequantize-then-fp32
   softmax(Q K^T * sm_scale) V that ``ref_kernel`` (TASK/reference.py:349-369)
   approximates through AITER, gathered through ``kv_indices`` (page size 1).
+* ``absorb_q`` / ``v_up_proj``  -- the neighbouring per-head products the
+  reference names but does not implement (mixed-mla/README.md:213-217): the
+  W_UK absorption that produces the decode's 576-wide Q and the v_up_proj
+  lift of its 512-wide output, in float32 from bf16 operands.
 
 Independence from the kernels: the element encoders here are *table searches*
 (nearest representable value, ties to the even code), not the bit tricks the
@@ -44,6 +48,8 @@ Parity pins (see tests/test_oracle_*.py):
                  row permutation; saturation and exact-grid closed forms.
   attention   -- float64 brute force on tiny shapes, closed forms (kv_len=1,
                  identical keys), permutation/split invariance.
+  neighbours  -- float64 brute force on tiny shapes; identity-block weights
+                 reproduce the input columns; the rope columns pass through.
 """
 from __future__ import annotations
 
@@ -445,3 +451,24 @@ def bf16_tensor_bits(t) -> np.ndarray:
 
 def default_sm_scale() -> float:
     return 1.0 / math.sqrt(QK_DIM)
+
+
+# ----------------------------------------------------------------------------
+# Neighbouring steps: W_UK absorption (upstream) and v_up_proj (downstream)
+# ----------------------------------------------------------------------------
+def absorb_q(q_nope_bits: np.ndarray, q_rope_bits: np.ndarray, w_uk_bits: np.ndarray) -> np.ndarray:
+    """bf16 bits q_nope [B, H, 128], q_rope [B, H, 64], w_uk [H, 128, 512] ->
+    float32 Q [B, H, 576] = [q_nope[b, h] @ w_uk[h], q_rope[b, h]]."""
+    qn = bf16_to_f32(q_nope_bits).astype(np.float32)
+    w = bf16_to_f32(w_uk_bits).astype(np.float32)
+    lat = np.einsum("bhk,hkn->bhn", qn, w, optimize=True).astype(np.float32)
+    return np.concatenate([lat, bf16_to_f32(q_rope_bits).astype(np.float32)], axis=-1)
+
+
+def v_up_proj(o_bits: np.ndarray, w_uv_bits: np.ndarray) -> np.ndarray:
+    """bf16 bits o [B, H, 512], w_uv [H, 512, 128] -> float32 [B, H, 128]
+    = o[b, h] @ w_uv[h]."""
+    o = bf16_to_f32(o_bits).astype(np.float32)
+    w = bf16_to_f32(w_uv_bits).astype(np.float32)
+    return np.einsum("bhk,hkn->bhn", o, w, optimize=True).astype(np.float32)
+
