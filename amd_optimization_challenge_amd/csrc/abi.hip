@@ -393,6 +393,50 @@ int mla_decode_fwd(const void* q_bf16, const void* k_cache, int64_t k_row_stride
   return MLA_OK;
 }
 
+int mla_absorb_q(const void* q_nope, const void* q_rope, const void* w_uk, int batch, int num_heads,
+                 void* q_out, void* stream) {
+  if (batch < 1 || num_heads < 1 || num_heads > 65535)
+    return fail(MLA_ERR_INVALID_ARGUMENT, "batch must be >= 1 and num_heads in [1, 65535] (got %d, %d)", batch,
+                num_heads);
+  if (!q_nope || !q_rope || !w_uk || !q_out) return fail(MLA_ERR_INVALID_ARGUMENT, "null pointer argument");
+  if (!aligned(q_nope, 16) || !aligned(q_rope, 16) || !aligned(w_uk, 16) || !aligned(q_out, 16))
+    return fail(MLA_ERR_INVALID_ARGUMENT, "q_nope, q_rope, w_uk and q_out must be 16-byte aligned");
+  hipError_t e = launch_absorb_q(static_cast<const uint16_t*>(q_nope), static_cast<const uint16_t*>(q_rope),
+                                 static_cast<const uint16_t*>(w_uk), batch, num_heads,
+                                 static_cast<uint16_t*>(q_out), static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "absorb launch");
+  return MLA_OK;
+}
+
+int mla_v_up_proj(const void* o, const void* w_uv, int batch, int num_heads, void* y_bf16, void* out_fp8,
+                  float* out_scale, void* workspace, int64_t workspace_bytes, void* stream) {
+  if (batch < 1 || num_heads < 1 || 2 * num_heads > kAmaxMaxBlocks)
+    return fail(MLA_ERR_INVALID_ARGUMENT, "batch must be >= 1 and num_heads in [1, %d] (got %d, %d)",
+                kAmaxMaxBlocks / 2, batch, num_heads);
+  if (!o || !w_uv || !y_bf16) return fail(MLA_ERR_INVALID_ARGUMENT, "null pointer argument");
+  if (!aligned(o, 16) || !aligned(w_uv, 16) || !aligned(y_bf16, 16))
+    return fail(MLA_ERR_INVALID_ARGUMENT, "o, w_uv and y must be 16-byte aligned");
+  const bool fp8 = out_fp8 != nullptr;
+  if (fp8) {
+    if (!out_scale || !workspace) return fail(MLA_ERR_INVALID_ARGUMENT, "the fp8 output needs out_scale and workspace");
+    if (!aligned(out_fp8, 8) || !aligned(workspace, 16))
+      return fail(MLA_ERR_INVALID_ARGUMENT, "out_fp8 must be 8-byte and workspace 16-byte aligned");
+    if (workspace_bytes < kQuantScratchBytes)
+      return fail(MLA_ERR_WORKSPACE_TOO_SMALL, "workspace needs %lld bytes", (long long)kQuantScratchBytes);
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  uint32_t* partials = fp8 ? static_cast<uint32_t*>(workspace) : nullptr;
+  hipError_t e = launch_v_up_proj(static_cast<const uint16_t*>(o), static_cast<const uint16_t*>(w_uv), batch,
+                                  num_heads, static_cast<uint16_t*>(y_bf16), partials, s);
+  if (e != hipSuccess) return hip_fail(e, "v_up_proj launch");
+  if (fp8) {
+    e = launch_quant_fp8(static_cast<const uint16_t*>(y_bf16), (int64_t)batch * num_heads * 128, partials,
+                         2 * num_heads, static_cast<uint8_t*>(out_fp8), out_scale, s);
+    if (e != hipSuccess) return hip_fail(e, "quant launch");
+  }
+  return MLA_OK;
+}
+
 int mla_selftest(int which, const void* in, void* out, void* stream) {
   if (!in || !out) return fail(MLA_ERR_INVALID_ARGUMENT, "null pointer argument");
   hipError_t e = launch_selftest(which, in, out, static_cast<hipStream_t>(stream));

@@ -50,6 +50,12 @@ hipError_t launch_append_kv(const uint16_t* x, int64_t n, int64_t x_stride, cons
 hipError_t launch_decode(const DecodeParams& p, int kv_mode, int grid, hipStream_t stream);
 hipError_t launch_combine(const DecodeParams& p, hipStream_t stream);
 
+// neighbours.hip
+hipError_t launch_absorb_q(const uint16_t* q_nope, const uint16_t* q_rope, const uint16_t* w_uk, int batch,
+                           int heads, uint16_t* q_out, hipStream_t stream);
+hipError_t launch_v_up_proj(const uint16_t* o, const uint16_t* w_uv, int batch, int heads, uint16_t* y,
+                            uint32_t* amax_partials, hipStream_t stream);
+
 // selftest.hip
 hipError_t launch_selftest(int which, const void* in, void* out, hipStream_t stream);
 

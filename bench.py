@@ -265,8 +265,21 @@ def bench_neighbours(steps, warmup):
         w_uk = (torch.randn((H, 128, 512), generator=g) / 11.3).to(torch.bfloat16).cuda()
         o = torch.randn((B, H, 512), generator=g).to(torch.bfloat16).cuda()
         w_uv = (torch.randn((H, 512, 128), generator=g) / 22.6).to(torch.bfloat16).cuda()
-        cases = [("absorb_q", lambda: N.absorb_q(qn, qr, w_uk), 2 * (H * 128 * 512 + B * H * 192 + B * H * 576)),
-                 ("v_up_proj", lambda: N.v_up_proj(o, w_uv), 2 * (H * 512 * 128 + B * H * 512 + B * H * 128)),
+        def bmm_absorb():  # the library-GEMM formulation, timed beside the HIP kernel
+            q = torch.empty((B, H, 576), dtype=torch.bfloat16, device=qn.device)
+            q[..., :512] = torch.bmm(qn.transpose(0, 1).contiguous(), w_uk).transpose(0, 1)
+            q[..., 512:] = qr
+            return q
+
+        def bmm_up():
+            return torch.bmm(o.transpose(0, 1).contiguous(), w_uv).transpose(0, 1).contiguous()
+
+        b_absorb = 2 * (H * 128 * 512 + B * H * 192 + B * H * 576)
+        b_up = 2 * (H * 512 * 128 + B * H * 512 + B * H * 128)
+        cases = [("absorb_q", lambda: N.absorb_q(qn, qr, w_uk), b_absorb),
+                 ("absorb_q torch.bmm", bmm_absorb, b_absorb),
+                 ("v_up_proj", lambda: N.v_up_proj(o, w_uv), b_up),
+                 ("v_up_proj torch.bmm", bmm_up, b_up),
                  ("v_up_proj+fp8", lambda: N.v_up_proj(o, w_uv, quant_fp8=True),
                   2 * (H * 512 * 128 + B * H * 512) + B * H * 128)]
         for name, fn, nbytes in cases:

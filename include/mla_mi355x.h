@@ -89,6 +89,27 @@ int mla_pack_mxfp4(const void* x_bf16, int64_t rows, int cols, int64_t x_row_str
                    int64_t scale_row_stride, void* stream);
 
 /*
+ * W_UK absorption, the step before the decode: q_out [batch, H, 576] bf16 =
+ * [q_nope[b, h] @ w_uk[h], q_rope[b, h]] for q_nope [batch, H, 128], q_rope
+ * [batch, H, 64], w_uk [H, 128, 512] (bf16, contiguous, 16-byte aligned); f32
+ * accumulation, one bf16 rounding.  The reference names this step of
+ * DeepSeek-style MLA but has no implementation of it (mixed-mla/README.md:213-217).
+ */
+int mla_absorb_q(const void* q_nope, const void* q_rope, const void* w_uk, int batch, int num_heads,
+                 void* q_out, void* stream);
+
+/*
+ * v_up_proj, the step after the decode: y_bf16 [batch, H, 128] = o[b, h] @
+ * w_uv[h] for o [batch, H, 512] (the decode output), w_uv [H, 512, 128] (bf16,
+ * contiguous, 16-byte aligned), 1 <= H <= 512.  out_fp8 (optional): the
+ * per-tensor FP8 quantization of y_bf16, as mla_quant_fp8_per_tensor gives it,
+ * with its scale in out_scale[0]; it needs a workspace of >= 8 KiB.  No
+ * counterpart in the reference, which names the step (mixed-mla/README.md:213-217).
+ */
+int mla_v_up_proj(const void* o, const void* w_uv, int batch, int num_heads, void* y_bf16, void* out_fp8,
+                  float* out_scale, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
  * KV-cache append: writes n new tokens (bf16 [n, 576], row stride in bytes)
  * into cache rows slots[i] (page size 1; slots == NULL means row i; a negative
  * slot skips its token; slots must be distinct; n <= 29826161 per call).

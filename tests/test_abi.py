@@ -40,6 +40,13 @@ def test_argument_errors_without_device():
     assert lib.mla_pack_mxfp4(None, 4, 33, 66, None, 16, None, 2, None) == _lib.MLA_ERR_INVALID_ARGUMENT
     assert lib.mla_quant_fp8_per_tensor(None, 0, None, None, None, 0, None) == _lib.MLA_ERR_INVALID_ARGUMENT
     assert lib.mla_selftest(0, None, None, None) == _lib.MLA_ERR_INVALID_ARGUMENT
+    # neighbouring steps: bad sizes, null pointers, fp8 output without its workspace
+    assert lib.mla_absorb_q(16, 16, 16, 0, 16, 16, None) == _lib.MLA_ERR_INVALID_ARGUMENT
+    assert lib.mla_absorb_q(None, 16, 16, 4, 16, 16, None) == _lib.MLA_ERR_INVALID_ARGUMENT
+    assert lib.mla_v_up_proj(16, 16, 4, 513, 16, None, None, None, 0, None) == _lib.MLA_ERR_INVALID_ARGUMENT
+    assert b"512" in lib.mla_last_error()
+    assert lib.mla_v_up_proj(16, 16, 4, 16, 16, 16, 16, None, 0, None) == _lib.MLA_ERR_INVALID_ARGUMENT
+    assert lib.mla_v_up_proj(16, 16, 4, 16, 16, 16, 16, 16, 4096, None) == _lib.MLA_ERR_WORKSPACE_TOO_SMALL
     # append: no cache, negative n, fp8 cache without its scale, short scale stride
     assert lib.mla_append_kv(None, 4, 1152, None, None, 0, None, None, 0, None, 0, None,
                              None) == _lib.MLA_ERR_INVALID_ARGUMENT

@@ -21,7 +21,7 @@ def _close_bf16(got, ref):
     assert np.all(err <= 2 ** -7 * np.abs(ref_b) + 2 ** -12 * scale), float(err.max())
 
 
-@pytest.mark.parametrize("B,H", [(4, 16), (64, 128), (37, 16)])
+@pytest.mark.parametrize("B,H", [(4, 16), (64, 128), (37, 16), (1, 128), (130, 16)])
 def test_absorb_q_matches_oracle(cuda, B, H):
     print(f"absorb_q B={B} H={H}", flush=True)
     g = torch.Generator().manual_seed(B * 7 + H)
@@ -35,7 +35,7 @@ def test_absorb_q_matches_oracle(cuda, B, H):
     assert torch.equal(got[..., 512:].cpu(), qr)
 
 
-@pytest.mark.parametrize("B,H", [(4, 16), (64, 128)])
+@pytest.mark.parametrize("B,H", [(4, 16), (64, 128), (1, 16), (37, 128), (130, 16)])
 def test_v_up_proj_and_fp8_match_oracle(cuda, B, H):
     print(f"v_up_proj B={B} H={H}", flush=True)
     g = torch.Generator().manual_seed(B + 3 * H)
@@ -50,6 +50,7 @@ def test_v_up_proj_and_fp8_match_oracle(cuda, B, H):
     codes, s = O.quantize_fp8_per_tensor(O.bf16_tensor_bits(y.cpu()))
     assert np.array_equal(q8.view(torch.uint8).cpu().numpy(), codes.reshape(q8.shape))
     assert float(sc) == float(s)
+    assert torch.equal(y, N.v_up_proj(o.cuda(), w.cuda()))  # deterministic: same bits again
 
 
 def test_absorb_decode_up_chain(cuda):
