@@ -410,9 +410,9 @@ int mla_absorb_q(const void* q_nope, const void* q_rope, const void* w_uk, int b
 
 int mla_v_up_proj(const void* o, const void* w_uv, int batch, int num_heads, void* y_bf16, void* out_fp8,
                   float* out_scale, void* workspace, int64_t workspace_bytes, void* stream) {
-  if (batch < 1 || num_heads < 1 || 2 * num_heads > kAmaxMaxBlocks)
+  if (batch < 1 || num_heads < 1 || num_heads > kUpProjMaxHeads)
     return fail(MLA_ERR_INVALID_ARGUMENT, "batch must be >= 1 and num_heads in [1, %d] (got %d, %d)",
-                kAmaxMaxBlocks / 2, batch, num_heads);
+                kUpProjMaxHeads, batch, num_heads);
   if (!o || !w_uv || !y_bf16) return fail(MLA_ERR_INVALID_ARGUMENT, "null pointer argument");
   if (!aligned(o, 16) || !aligned(w_uv, 16) || !aligned(y_bf16, 16))
     return fail(MLA_ERR_INVALID_ARGUMENT, "o, w_uv and y must be 16-byte aligned");
@@ -426,12 +426,13 @@ int mla_v_up_proj(const void* o, const void* w_uv, int batch, int num_heads, voi
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
   uint32_t* partials = fp8 ? static_cast<uint32_t*>(workspace) : nullptr;
+  int nparts = 0;
   hipError_t e = launch_v_up_proj(static_cast<const uint16_t*>(o), static_cast<const uint16_t*>(w_uv), batch,
-                                  num_heads, static_cast<uint16_t*>(y_bf16), partials, s);
+                                  num_heads, static_cast<uint16_t*>(y_bf16), partials, &nparts, s);
   if (e != hipSuccess) return hip_fail(e, "v_up_proj launch");
   if (fp8) {
     e = launch_quant_fp8(static_cast<const uint16_t*>(y_bf16), (int64_t)batch * num_heads * 128, partials,
-                         2 * num_heads, static_cast<uint8_t*>(out_fp8), out_scale, s);
+                         nparts, static_cast<uint8_t*>(out_fp8), out_scale, s);
     if (e != hipSuccess) return hip_fail(e, "quant launch");
   }
   return MLA_OK;

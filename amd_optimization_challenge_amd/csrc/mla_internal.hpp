@@ -54,7 +54,10 @@ hipError_t launch_combine(const DecodeParams& p, hipStream_t stream);
 hipError_t launch_absorb_q(const uint16_t* q_nope, const uint16_t* q_rope, const uint16_t* w_uk, int batch,
                            int heads, uint16_t* q_out, hipStream_t stream);
 hipError_t launch_v_up_proj(const uint16_t* o, const uint16_t* w_uv, int batch, int heads, uint16_t* y,
-                            uint32_t* amax_partials, hipStream_t stream);
+                            uint32_t* amax_partials, int* nparts, hipStream_t stream);
+// Largest head count of v_up_proj with the FP8 output (one partial max per
+// head and 32-column slice, kAmaxMaxBlocks in all).
+constexpr int kUpProjMaxHeads = kAmaxMaxBlocks / 4;
 
 // selftest.hip
 hipError_t launch_selftest(int which, const void* in, void* out, hipStream_t stream);

@@ -101,7 +101,7 @@ int mla_absorb_q(const void* q_nope, const void* q_rope, const void* w_uk, int b
 /*
  * v_up_proj, the step after the decode: y_bf16 [batch, H, 128] = o[b, h] @
  * w_uv[h] for o [batch, H, 512] (the decode output), w_uv [H, 512, 128] (bf16,
- * contiguous, 16-byte aligned), 1 <= H <= 512.  out_fp8 (optional): the
+ * contiguous, 16-byte aligned), 1 <= H <= 256.  out_fp8 (optional): the
  * per-tensor FP8 quantization of y_bf16, as mla_quant_fp8_per_tensor gives it,
  * with its scale in out_scale[0]; it needs a workspace of >= 8 KiB.  No
  * counterpart in the reference, which names the step (mixed-mla/README.md:213-217).

@@ -43,8 +43,8 @@ def test_argument_errors_without_device():
     # neighbouring steps: bad sizes, null pointers, fp8 output without its workspace
     assert lib.mla_absorb_q(16, 16, 16, 0, 16, 16, None) == _lib.MLA_ERR_INVALID_ARGUMENT
     assert lib.mla_absorb_q(None, 16, 16, 4, 16, 16, None) == _lib.MLA_ERR_INVALID_ARGUMENT
-    assert lib.mla_v_up_proj(16, 16, 4, 513, 16, None, None, None, 0, None) == _lib.MLA_ERR_INVALID_ARGUMENT
-    assert b"512" in lib.mla_last_error()
+    assert lib.mla_v_up_proj(16, 16, 4, 257, 16, None, None, None, 0, None) == _lib.MLA_ERR_INVALID_ARGUMENT
+    assert b"256" in lib.mla_last_error()
     assert lib.mla_v_up_proj(16, 16, 4, 16, 16, 16, 16, None, 0, None) == _lib.MLA_ERR_INVALID_ARGUMENT
     assert lib.mla_v_up_proj(16, 16, 4, 16, 16, 16, 16, 16, 4096, None) == _lib.MLA_ERR_WORKSPACE_TOO_SMALL
     # append: no cache, negative n, fp8 cache without its scale, short scale stride
