@@ -190,6 +190,13 @@ def test_fused_pipeline_matches_staged(cuda, heads, mode):
     torch.cuda.synchronize()
     assert torch.equal(outs[0], fused)
     assert torch.equal(outs[1], fused)
+    # the whole operator on a workspace of garbage bytes, twice in a row: the
+    # call owns every workspace word it reads
+    ws2 = torch.full_like(ws, 0x5A)
+    for _ in range(2):
+        out = ops.decode_fwd(qd, kv_data, kv_indptr, cfg["kv_indices"], cfg["sm_scale"], mode, ws=ws2)
+        torch.cuda.synchronize()
+        assert torch.equal(out, fused)
 
 
 def _lse_close(got, ref, tol=1e-2):

@@ -32,6 +32,7 @@ def test_plan_covers_every_token_once(cuda, lens, heads, mode):
     indptr[1:] = torch.cumsum(torch.tensor(lens), 0)
     ws = ops.workspace(B, heads, mode, cuda)
     assert ws.numel() == ops.workspace_layout(B, heads, mode, ops.cu_count())["total"]
+    ws.fill_(0x5A)  # the planner owns every word it reads back
     ops.plan(indptr.cuda(), B, heads, mode, ws)
     torch.cuda.synchronize()
     P = ops.read_plan(ws, B, heads, mode)
