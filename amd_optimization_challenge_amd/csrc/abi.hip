@@ -74,19 +74,18 @@ int check_shape(int batch, int num_heads, int kv_mode) {
 
 }  // namespace
 
-// Items the planner aims for: one per resident work-group slot (H=16 fp8-V
-// kernels fit two per CU, the others one), raised to 2 per sequence when the
-// batch is large so long sequences still get split, capped at 4 rounds.
-// Resident decode work-groups per CU: two for H = 16 with the fp8 cache (a
-// two-stage ring), one otherwise (the LDS ring fills the CU).  kv_mode < 0
-// asks for the largest over the modes (the workspace is sized for it).
-// resident decode work-groups per CU: 2 for H = 16 with one cache (fp8 or
-// mxfp4 rows serve both K and V), else 1; kv_mode < 0 gives the largest
+// Resident decode work-groups per CU: two for H = 16 with one cache (fp8 or
+// mxfp4 rows serve both K and V; the ring fits in half the LDS), else one (the
+// LDS ring fills the CU).  kv_mode < 0 gives the largest over the modes (the
+// workspace is sized for it).
 static int blocks_per_cu(int num_heads, int kv_mode) {
   if (num_heads != 16) return 1;
   return (kv_mode == MLA_KV_FP8 || kv_mode == MLA_KV_MXFP4 || kv_mode < 0) ? 2 : 1;
 }
 
+// Items the planner aims for: one per resident work-group slot, raised to two
+// per sequence when the batch is large so long sequences still get split,
+// capped at four rounds of slots.
 int target_items_for(int batch, int num_heads, int kv_mode, int num_cu) {
   const int slots = num_cu * blocks_per_cu(num_heads, kv_mode);
   int t = 2 * batch > slots ? 2 * batch : slots;
