@@ -33,10 +33,6 @@ constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kPScale = 256.0f;  // fp8 P = p * 256
 constexpr float kRebase = 96.0f;   // H128: max log2 distance of a tile max above the fixed reference
 
-__device__ __forceinline__ int kv_slot(const int32_t* __restrict__ idx, int pos) {
-  return idx != nullptr ? idx[pos] : pos;
-}
-
 __device__ __forceinline__ v8i ld_v8(const uint8_t* p) {
   uint4 a = *reinterpret_cast<const uint4*>(p);
   uint4 b = *reinterpret_cast<const uint4*>(p + 16);
@@ -51,9 +47,6 @@ __device__ __forceinline__ v8i ld_v4_as_v8(const uint8_t* p) {
   r[0] = a.x; r[1] = a.y; r[2] = a.z; r[3] = a.w;
   r[4] = 0; r[5] = 0; r[6] = 0; r[7] = 0;
   return r;
-}
-__device__ __forceinline__ uint4 ldg16(const uint8_t* p) {
-  return ldg16_nt(p);
 }
 __device__ __forceinline__ float neg_inf() { return -__builtin_inff(); }
 
