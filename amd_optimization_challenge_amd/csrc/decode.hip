@@ -177,11 +177,11 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
 
   // ---- ring issue ----------------------------------------------------------
   // slots of tile t live in slot stage t % NSL
-  auto slot_of = [&](int t, int tok) -> int {
+  auto slot_of = [&](int t, int tok) -> int __attribute__((always_inline)) {
     if constexpr (IDX) return reinterpret_cast<const int*>(smem + C::OFF_SLOT + (t % C::NSL) * 256)[tok];
     else return min(t_beg + kTile * t + tok, t_end - 1);
   };
-  auto issue_slots = [&](int t) {  // wave 0: the 64 slots of tile t (positions clamped into the item)
+  auto issue_slots = [&](int t) __attribute__((always_inline)) {  // wave 0: the 64 slots of tile t (positions clamped into the item)
     if constexpr (IDX) {
       if (w == 0) {
         const int pos = min(t_beg + kTile * t + lane, t_end - 1);
@@ -189,7 +189,7 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
       }
     }
   };
-  auto issue_rows = [&](int t) {  // row waves: windows u = (w - RW0) + NRW k of tile t
+  auto issue_rows = [&](int t) __attribute__((always_inline)) {  // row waves: windows u = (w - RW0) + NRW k of tile t
     if (w < C::RW0) return;
     const int st = t % C::S;
     const uint32_t sbase = lds0 + st * C::STAGE;
@@ -221,7 +221,7 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
   // and instruction; byte j lands in dword j * 64 + lane of the tile's scale
   // stage (sub-dword LDS-DMA writes one dword per lane).  Byte columns j = w +
   // SCW k are this wave's.
-  auto issue_scales = [&](int t) {
+  auto issue_scales = [&](int t) __attribute__((always_inline)) {
     if constexpr (KF == 1) {
       if (w < C::SCW) {
         const uint8_t* srow = p.k_scales + (int64_t)slot_of(t, lane) * p.k_scale_stride;
@@ -235,7 +235,7 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
     }
   };
   // this wave's wait for tile t's rows (and scales), k groups issued after them
-  auto wait_tile = [&](int k) {
+  auto wait_tile = [&](int k) __attribute__((always_inline)) {
     constexpr int SL = IDX ? 1 : 0;  // wave 0 issues one slot DMA per group
     if constexpr (KF == 1 && C::SCW == 4) {
       // rows: NA for waves < NAW, else NA - 1; scale columns: 5 for waves 0, 1, else 4
@@ -274,64 +274,70 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
   // g' where 32g + e = 16g' + (i & 15) + 64 (i >> 4); the fp8 Q operand is
   // gathered in that order.  With fp8 K both operands share one order.
   v8i qv[5];
-  float qs;
-  {
-    auto load_q = [&](const uint8_t* qrow) {
-      if constexpr (KF == 0) {
+  float c = 0.f;  // qs * kv scale (fp8 K) * sm_scale * log2(e), set once Q is resident
+  const float kvs = (KF == 0 || VF == 1) ? p.kv_scale[0] : 1.0f;
+  const float vscale = VF == 2 ? 1.0f : kvs;
+  auto load_q = [&](const uint8_t* qrow) __attribute__((always_inline)) {
+    if constexpr (KF == 0) {
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) qv[ks] = ld_v8(qrow + 128 * ks + 32 * g);
-        qv[4] = g < 2 ? ld_v8(qrow + 512 + 32 * g) : v8i{0, 0, 0, 0, 0, 0, 0, 0};
-      } else {
-#pragma unroll
-        for (int ks = 0; ks < 5; ++ks) {
-          const uint4 lo = *reinterpret_cast<const uint4*>(qrow + 128 * ks + 16 * g);
-          const uint4 hi = ks < 4 ? *reinterpret_cast<const uint4*>(qrow + 128 * ks + 64 + 16 * g)
-                                  : make_uint4(0, 0, 0, 0);
-          qv[ks] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-        }
-      }
-    };
-    if constexpr (QB) {
-      // Q quantized here (bit-exact with the quant kernel): the per-tensor
-      // scale is folded from the amax partials, and this sequence's 16 x 576
-      // fp8 Q is staged row-major in the last ring stage (its first DMA comes
-      // after the first tile barrier)
-      uint8_t* qst = smem + (C::S - 1) * C::STAGE;
-      const uint4* src = reinterpret_cast<const uint4*>(p.q_bf16 + (int64_t)b * 16 * kQKDim);
-      constexpr int NV = 16 * kQKDim / 8, NJ = (NV + 255) / 256;
-      uint4 xv[NJ];
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        const int i = tid + 256 * j;
-        if (i < NV) xv[j] = src[i];
-      }
-      uint32_t m = 0;
-      for (int i = tid; i < p.q_nparts; i += 256) m = max(m, p.q_partials[i]);
-      m = (uint32_t)wave_max((int)m);
-      uint32_t* xu = reinterpret_cast<uint32_t*>(smem + C::OFF_X);
-      if (lane == 0) xu[w] = m;
-      lds_barrier();
-      qs = fp8_scale_from_amax(max(max(xu[0], xu[1]), max(xu[2], xu[3])));
-      const Fp8Quant qq = make_fp8_quant(qs);
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        const int i = tid + 256 * j;
-        if (i < NV) {
-          *reinterpret_cast<uint2*>(qst + 8 * i) = quant8_fp8(xv[j], qq);
-        }
-      }
-      lds_barrier();
-      load_q(qst + l16 * kQKDim);
+      for (int ks = 0; ks < 4; ++ks) qv[ks] = ld_v8(qrow + 128 * ks + 32 * g);
+      qv[4] = g < 2 ? ld_v8(qrow + 512 + 32 * g) : v8i{0, 0, 0, 0, 0, 0, 0, 0};
     } else {
-      qs = p.q_scale[0];
-      load_q(p.q_fp8 + ((int64_t)b * 16 + l16) * kQKDim);
+#pragma unroll
+      for (int ks = 0; ks < 5; ++ks) {
+        const uint4 lo = *reinterpret_cast<const uint4*>(qrow + 128 * ks + 16 * g);
+        const uint4 hi = ks < 4 ? *reinterpret_cast<const uint4*>(qrow + 128 * ks + 64 + 16 * g)
+                                : make_uint4(0, 0, 0, 0);
+        qv[ks] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+      }
     }
 #pragma unroll
     for (int ks = 0; ks < 5; ++ks) asm volatile("" : "+v"(qv[ks]));  // keep resident, no reload
+  };
+  // QB: Q is quantized here, bit-exact with the quant kernel.  This sequence's
+  // 16 x 576 bf16 Q (18 KiB) is gathered by LDS-DMA into the last ring stage
+  // and the per-tensor amax partials are loaded, in flight with the first slot
+  // indices; quantize_q folds the scale and quantizes in place once the first
+  // prologue has issued the rows of every other stage, and the fp8 Q fragments
+  // are read before the last stage's rows are issued.
+  constexpr int QNV = 16 * kQKDim / 8, QNJ = (QNV + 255) / 256;  // 16-B bf16 chunks, per thread
+  static_assert(C::STAGE >= 16 * kQKDim * 2, "bf16 Q fits one ring stage");
+  const uint32_t qlds = lds0 + (C::S - 1) * C::STAGE;
+  uint32_t qm = 0;
+  if constexpr (QB) {
+    const uint8_t* src = reinterpret_cast<const uint8_t*>(p.q_bf16 + (int64_t)b * 16 * kQKDim);
+    for (int k = w; k < QNV / 64; k += 4) dma16_to_lds(src + 1024 * k + 16 * lane, qlds + 1024 * k);
+    for (int i = tid; i < p.q_nparts; i += 256) qm = max(qm, p.q_partials[i]);
+  } else {
+    load_q(p.q_fp8 + ((int64_t)b * 16 + l16) * kQKDim);
+    c = p.q_scale[0] * (KF == 0 ? kvs : 1.0f) * p.sm_scale * kLog2e;
   }
-  const float kvs = (KF == 0 || VF == 1) ? p.kv_scale[0] : 1.0f;
-  const float c = qs * (KF == 0 ? kvs : 1.0f) * p.sm_scale * kLog2e;
-  const float vscale = VF == 2 ? 1.0f : kvs;
+  auto quantize_q = [&]() __attribute__((always_inline)) {  // block-uniform; the loads have landed
+    if constexpr (QB) {
+      uint8_t* qst = smem + (C::S - 1) * C::STAGE;
+      uint32_t* xu = reinterpret_cast<uint32_t*>(smem + C::OFF_X);
+      const uint32_t m = (uint32_t)wave_max((int)qm);
+      if (lane == 0) xu[w] = m;
+      uint4 xv[QNJ];
+#pragma unroll
+      for (int j = 0; j < QNJ; ++j) {
+        const int i = tid + 256 * j;
+        if (i < QNV) xv[j] = *reinterpret_cast<const uint4*>(qst + 16 * i);
+      }
+      lds_barrier();  // partial maxima exchanged; every bf16 chunk read before the fp8 rows overwrite them
+      const float qs = fp8_scale_from_amax(max(max(xu[0], xu[1]), max(xu[2], xu[3])));
+      const Fp8Quant qq = make_fp8_quant(qs);
+#pragma unroll
+      for (int j = 0; j < QNJ; ++j) {
+        const int i = tid + 256 * j;
+        if (i < QNV) *reinterpret_cast<uint2*>(qst + 8 * i) = quant8_fp8(xv[j], qq);
+      }
+      lds_barrier();
+      load_q(qst + l16 * kQKDim);
+      lds_barrier();  // every wave holds its fragments before the stage is refilled
+      c = qs * (KF == 0 ? kvs : 1.0f) * p.sm_scale * kLog2e;
+    }
+  };
 
   v4f o[8];
 #pragma unroll
@@ -340,7 +346,7 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
   bool have_ref = false;
   int e_ref = 127, e_seen = 0;  // fp4 V: reference and running max of the V block exponents
 
-  auto prologue = [&](bool slots_issued) {
+  auto prologue = [&](bool slots_issued, bool quant) __attribute__((always_inline)) {
     if (!slots_issued) {
 #pragma unroll
       for (int j = 0; j < C::S; ++j) issue_slots(j);
@@ -350,20 +356,24 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
 #pragma unroll
     for (int j = 0; j < C::S; ++j) {
       if (j >= ntiles) break;
+      if (quant && j == C::S - 1) quantize_q();  // the other stages' rows are in flight
       issue_slots(j + C::S);
       issue_rows(j);
       issue_scales(j);
     }
+    if (quant && ntiles < C::S) quantize_q();  // the last stage stays free
   };
 
   // ---- main loop ---------------------------------------------------------------
   int8_t* vote = reinterpret_cast<int8_t*>(smem + C::OFF_VOTE);
   float* xch = reinterpret_cast<float*>(smem + C::OFF_X);
   bool slots_issued = true;  // by the early issue above; a restart issues them again
+  bool q_pending = QB;       // Q is quantized in the first prologue only
   for (;;) {
     bool restart = false;
-    if (ntiles > 0) prologue(slots_issued);
+    if (ntiles > 0) prologue(slots_issued, q_pending);
     slots_issued = false;
+    q_pending = false;
     for (int ti = 0; ti < ntiles; ++ti) {
       const int st = ti % C::S;
       const int nval = min(kTile, ntok - kTile * ti);
