@@ -34,6 +34,8 @@ WsLayout workspace_layout(int batch, int num_heads, int kv_mode, int num_cu);
 hipError_t launch_amax(const uint16_t* x, int64_t n, uint32_t* partials, int* nblocks,
                        const int32_t* kv_indptr, const int32_t* kv_indices, int batch, int qlen,
                        int target_items, int max_items, int32_t* plan, hipStream_t stream);
+// partials: 16-byte aligned, nblocks <= kAmaxMaxBlocks maxima (read four at a
+// time, so up to three words past nblocks are read and ignored)
 hipError_t launch_quant_fp8(const uint16_t* x, int64_t n, const uint32_t* partials, int nblocks,
                             uint8_t* out, float* out_scale, hipStream_t stream);
 hipError_t launch_pack_mxfp4(const uint16_t* x, int64_t rows, int cols, int64_t x_stride,

@@ -18,8 +18,8 @@ namespace mla {
 // pass 1: block-partial |x| max over bf16 (bit patterns: |x| ordering equals
 // unsigned ordering of (bits & 0x7fff) for non-NaN inputs)
 // ---------------------------------------------------------------------------
-__device__ void build_plan(const int32_t* __restrict__ kv_indptr, int batch, int qlen, int target_items,
-                           int max_items, int32_t* __restrict__ plan);
+__device__ __forceinline__ void build_plan(const int32_t* __restrict__ kv_indptr, int batch, int qlen,
+                                           int target_items, int max_items, int32_t* __restrict__ plan);
 
 __global__ __launch_bounds__(256) void amax_kernel(const uint16_t* __restrict__ x, int64_t n,
                                                    uint32_t* __restrict__ partials, int nblocks,
@@ -71,8 +71,19 @@ __global__ __launch_bounds__(256) void quant_fp8_kernel(const uint16_t* __restri
                                                         float* __restrict__ out_scale) {
   __shared__ float s_scale;
   __shared__ uint32_t red[4];
+  const int64_t nvec = n >> 3;
+  const uint4* xv = reinterpret_cast<const uint4*>(x);
+  // this thread's first 8 inputs are loaded while the partial maxima are folded
+  const int64_t i0 = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const uint4 first = i0 < nvec ? xv[i0] : make_uint4(0, 0, 0, 0);
+  // nparts <= kAmaxMaxBlocks = 4 x 256: one 16-byte load per thread
   uint32_t m = 0;
-  for (int i = threadIdx.x; i < nparts; i += 256) m = max(m, partials[i]);
+  if (4 * (int)threadIdx.x < nparts) {
+    const uint4 pv = reinterpret_cast<const uint4*>(partials)[threadIdx.x];
+    const int k = nparts - 4 * (int)threadIdx.x;
+    m = max(pv.x, k > 1 ? pv.y : 0u);
+    m = max(m, max(k > 2 ? pv.z : 0u, k > 3 ? pv.w : 0u));
+  }
   m = (uint32_t)wave_max((int)m);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
   __syncthreads();
@@ -83,12 +94,18 @@ __global__ __launch_bounds__(256) void quant_fp8_kernel(const uint16_t* __restri
   }
   __syncthreads();
   const Fp8Quant s = make_fp8_quant(s_scale);
-  const int64_t nvec = n >> 3;
-  const uint4* xv = reinterpret_cast<const uint4*>(x);
   uint2* ov = reinterpret_cast<uint2*>(out);
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < nvec; i += (int64_t)gridDim.x * 256) {
-    ov[i] = quant8_fp8(xv[i], s);
+  if (i0 < nvec) ov[i0] = quant8_fp8(first, s);
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  int64_t i = i0 + stride;
+  for (; i + 3 * stride < nvec; i += 4 * stride) {  // four loads in flight per thread
+    uint4 v[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) v[k] = xv[i + k * stride];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) ov[i + k * stride] = quant8_fp8(v[k], s);
   }
+  for (; i < nvec; i += stride) ov[i] = quant8_fp8(xv[i], s);
   for (int64_t i = (nvec << 3) + (int64_t)blockIdx.x * 256 + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * 256)
     out[i] = (uint8_t)quant_one(x[i], s);
@@ -334,8 +351,8 @@ __device__ __forceinline__ void emit_pieces(int4* __restrict__ items, int b, int
 // row's item count to its rank position and ds_bpermute to gather its first
 // item back), so the plan costs one round trip to kv_indptr and no barriers.
 // Same plan as the block version below.
-__device__ void build_plan_wave(const int32_t* __restrict__ kv_indptr, int batch, int qlen, int target_items,
-                                int max_items, int32_t* __restrict__ plan) {
+__device__ __forceinline__ void build_plan_wave(const int32_t* __restrict__ kv_indptr, int batch, int qlen,
+                                                int target_items, int max_items, int32_t* __restrict__ plan) {
   const int lane = threadIdx.x & 63;
   const bool act = lane < batch;
   const int s0 = act ? row_start(kv_indptr, lane, qlen) : 0;
@@ -354,10 +371,12 @@ __device__ void build_plan_wave(const int32_t* __restrict__ kv_indptr, int batch
   const int chunk = lo * 64;
   const int nb = act ? (L > 0 ? (L64 + lo - 1) / lo : 1) : 0;
   const int piece = act ? (L > 0 ? (L + nb - 1) / nb : 0) : -1;
-  // rank by piece length, longest first (ties by index); inactive lanes rank
-  // last.  The pieces are read lane by lane into scalar registers.
+  // rank by piece length, longest first (ties by index); inactive lanes (piece
+  // -1) never count and rank last.  All 64 lanes are read with constant lane
+  // indices, so the loop unrolls into independent readlanes.
   int rank = 0;
-  for (int b2 = 0; b2 < batch; ++b2) {
+#pragma unroll
+  for (int b2 = 0; b2 < 64; ++b2) {
     const int p2 = __builtin_amdgcn_readlane(piece, b2);
     rank += (p2 > piece) || (p2 == piece && b2 < lane);
   }
@@ -382,14 +401,14 @@ __device__ void build_plan_wave(const int32_t* __restrict__ kv_indptr, int batch
   }
 }
 
-__device__ void build_plan(const int32_t* __restrict__ kv_indptr, int batch, int qlen, int target_items,
-                           int max_items, int32_t* __restrict__ plan) {
+__device__ __forceinline__ void build_plan(const int32_t* __restrict__ kv_indptr, int batch, int qlen,
+                                           int target_items, int max_items, int32_t* __restrict__ plan) {
   if (batch <= 64) {
     if (threadIdx.x < 64) build_plan_wave(kv_indptr, batch, qlen, target_items, max_items, plan);
     return;
   }
   __shared__ int s_red[4];
-  __shared__ int s_piece[kPlanSortMax];  // piece length per sequence
+  __shared__ __attribute__((aligned(16))) int s_piece[kPlanSortMax];  // piece length per sequence
   __shared__ int s_cnt[kPlanSortMax];    // item counts in layout order, then their exclusive scan
   const int tid = threadIdx.x;
   int t_hi = 0, t_lo = 0, t_max = 0;
@@ -427,19 +446,24 @@ __device__ void build_plan(const int32_t* __restrict__ kv_indptr, int batch, int
   if (batch <= kPlanSortMax) {
     // rank sequences by piece length, longest first (ties by index)
     const int b = tid;
-    int L = 0, nb = 0, piece = 0;
+    int L = 0, nb = 0, piece = -1;  // -1: no sequence (never counts in a rank)
     if (b < batch) {
       L = len_of(b);
       nb = nb_of(L);
       piece = (L + nb - 1) / nb;
-      s_piece[b] = piece;
     }
+    if (b < kPlanSortMax) s_piece[b] = piece;
     __syncthreads();
     int rank = 0;
     if (b < batch) {
-      for (int b2 = 0; b2 < batch; ++b2) {
-        const int p2 = s_piece[b2];
-        rank += (p2 > piece) || (p2 == piece && b2 < b);
+      // four pieces per 16-byte LDS read, several reads in flight
+      const int4* pv = reinterpret_cast<const int4*>(s_piece);
+#pragma unroll 8
+      for (int b4 = 0; b4 < (batch + 3) / 4; ++b4) {
+        const int4 q = pv[b4];
+        const int p4[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) rank += (p4[k] > piece) || (p4[k] == piece && 4 * b4 + k < b);
       }
       s_cnt[rank] = nb;
     }
