@@ -408,7 +408,8 @@ __device__ __forceinline__ void build_plan(const int32_t* __restrict__ kv_indptr
     return;
   }
   __shared__ int s_red[4];
-  __shared__ __attribute__((aligned(16))) int s_piece[kPlanSortMax];  // piece length per sequence
+  // ordering key per sequence: piece length, then the lower index first
+  __shared__ __attribute__((aligned(16))) uint64_t s_key[kPlanSortMax];
   __shared__ int s_cnt[kPlanSortMax];    // item counts in layout order, then their exclusive scan
   const int tid = threadIdx.x;
   int t_hi = 0, t_lo = 0, t_max = 0;
@@ -452,18 +453,19 @@ __device__ __forceinline__ void build_plan(const int32_t* __restrict__ kv_indptr
       nb = nb_of(L);
       piece = (L + nb - 1) / nb;
     }
-    if (b < kPlanSortMax) s_piece[b] = piece;
+    // key = piece << 32 | (2^32 - 1 - b): a larger key ranks earlier, and
+    // "no sequence" (piece -1) is key 0, below every real one
+    const uint64_t key = piece < 0 ? 0ull : ((uint64_t)(uint32_t)piece << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)b);
+    if (b < kPlanSortMax) s_key[b] = key;
     __syncthreads();
     int rank = 0;
     if (b < batch) {
-      // four pieces per 16-byte LDS read, several reads in flight
-      const int4* pv = reinterpret_cast<const int4*>(s_piece);
+      // two keys per 16-byte LDS read, several reads in flight; one compare each
+      const ulonglong2* kv = reinterpret_cast<const ulonglong2*>(s_key);
 #pragma unroll 8
-      for (int b4 = 0; b4 < (batch + 3) / 4; ++b4) {
-        const int4 q = pv[b4];
-        const int p4[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-        for (int k = 0; k < 4; ++k) rank += (p4[k] > piece) || (p4[k] == piece && 4 * b4 + k < b);
+      for (int b2 = 0; b2 < (batch + 1) / 2; ++b2) {
+        const ulonglong2 q = kv[b2];
+        rank += (q.x > key) + (q.y > key);
       }
       s_cnt[rank] = nb;
     }
