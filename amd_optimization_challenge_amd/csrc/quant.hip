@@ -413,11 +413,13 @@ __device__ __forceinline__ void build_plan(const int32_t* __restrict__ kv_indptr
   __shared__ int s_cnt[kPlanSortMax];    // item counts in layout order, then their exclusive scan
   const int tid = threadIdx.x;
   int t_hi = 0, t_lo = 0, t_max = 0;
+  int own_s0 = 0;  // batch <= 256: this thread's row start (and t_max its length)
   for (int b = tid; b < batch; b += 256) {
     const int L = row_len(kv_indptr, b, qlen);
     t_hi += L >> 6;
     t_lo += L & 63;
     t_max = max(t_max, L);
+    own_s0 = row_start(kv_indptr, b, qlen);
   }
   const unsigned hi64 = (unsigned)block_sum(t_hi, s_red), lo64 = (unsigned)block_sum(t_lo, s_red);
   int chunk = 64 * max(kPlanMinChunk / 64, (int)tiles_per_item(hi64, lo64, target_items));
@@ -438,8 +440,7 @@ __device__ __forceinline__ void build_plan(const int32_t* __restrict__ kv_indptr
   auto nb_of = [&](int L) { return L > 0 ? (L + chunk - 1) / chunk : 1; };
   int4* items = reinterpret_cast<int4*>(plan + kPlanHeader);
   int2* binfo = reinterpret_cast<int2*>(plan + kPlanHeader + 4 * max_items);
-  auto emit = [&](int b, int L, int nb, int first) {
-    const int s0 = row_start(kv_indptr, b, qlen);
+  auto emit = [&](int b, int L, int nb, int first, int s0) {
     binfo[b] = make_int2(first, nb);
     emit_pieces(items, b, s0, L, nb, first);
   };
@@ -449,7 +450,7 @@ __device__ __forceinline__ void build_plan(const int32_t* __restrict__ kv_indptr
     const int b = tid;
     int L = 0, nb = 0, piece = -1;  // -1: no sequence (never counts in a rank)
     if (b < batch) {
-      L = len_of(b);
+      L = t_max;  // this thread's own row, read in the first pass
       nb = nb_of(L);
       piece = (L + nb - 1) / nb;
     }
@@ -475,7 +476,7 @@ __device__ __forceinline__ void build_plan(const int32_t* __restrict__ kv_indptr
     __syncthreads();
     if (tid < batch) s_cnt[tid] = ex;
     __syncthreads();
-    if (b < batch) emit(b, L, nb, s_cnt[rank]);
+    if (b < batch) emit(b, L, nb, s_cnt[rank], own_s0);
   } else {
     for (int base = 0; base < batch; base += 256) {
       const int b = base + tid;
@@ -486,7 +487,7 @@ __device__ __forceinline__ void build_plan(const int32_t* __restrict__ kv_indptr
       }
       int tot = 0;
       const int ex = block_exscan(nb, s_red, &tot);
-      if (b < batch) emit(b, L, nb, carry + ex);
+      if (b < batch) emit(b, L, nb, carry + ex, row_start(kv_indptr, b, qlen));
       carry += tot;
     }
   }
