@@ -621,6 +621,25 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
 }
 
 // ============================================================================
+// Q^T B-operand fragments of one lane of the H = 128 kernels: for K-step ks,
+// the 16 fp8 bytes at dims o = 64 ks + S0 hh and the 16 at o + D1 of the
+// lane's head row, kept resident in registers.
+// ============================================================================
+template <int S0, int D1>
+__device__ __forceinline__ void load_q128(const DecodeParams& p, int b, int head, int hh, v8i (&qv)[9]) {
+  const uint8_t* qrow = p.q_fp8 + ((int64_t)b * 128 + head) * kQKDim;
+#pragma unroll
+  for (int ks = 0; ks < 9; ++ks) {
+    const int o = 64 * ks + S0 * hh;
+    const uint4 lo = *reinterpret_cast<const uint4*>(qrow + o);
+    const uint4 hi = *reinterpret_cast<const uint4*>(qrow + o + D1);
+    qv[ks] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+  }
+#pragma unroll
+  for (int ks = 0; ks < 9; ++ks) asm volatile("" : "+v"(qv[ks]));  // keep resident, no reload
+}
+
+// ============================================================================
 // H = 128.  4 waves; wave w owns heads 32w .. 32w+31 for every token of the
 // work item and all 512 latent dims, so the softmax state and O^T never leave
 // the wave.  Q^T (the QK B operand) stays in registers, O^T in accumulators.
@@ -669,19 +688,7 @@ __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams 
 
   // ---- Q^T B operand, K-step ks = dims 64ks .. +63 (fp4 K partner order) -----
   v8i qv[9];
-  {
-    const uint8_t* qrow = p.q_fp8 + ((int64_t)b * 128 + head) * kQKDim;
-#pragma unroll
-    for (int ks = 0; ks < 9; ++ks) {
-      const int d0 = 64 * ks + 16 * hh;
-      const int d1 = d0 + 32;
-      const uint4 lo = *reinterpret_cast<const uint4*>(qrow + d0);
-      const uint4 hi = *reinterpret_cast<const uint4*>(qrow + d1);
-      qv[ks] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-    }
-#pragma unroll
-    for (int ks = 0; ks < 9; ++ks) asm volatile("" : "+v"(qv[ks]));
-  }
+  load_q128<16, 32>(p, b, head, hh, qv);
   const float qs = p.q_scale[0];
   const float kvs = p.kv_scale[0];
   const float c = qs * p.sm_scale * kLog2e;  // K's scales ride on the MFMA's A scale
@@ -1037,17 +1044,7 @@ __global__ __launch_bounds__(256, 1) void decode_h128p_kernel(const DecodeParams
 
   // ---- Q^T B operand, K-step ks = dims 64ks .. +63 -------------------------------
   v8i qv[9];
-  {
-    const uint8_t* qrow = p.q_fp8 + ((int64_t)b * 128 + head) * kQKDim;
-#pragma unroll
-    for (int ks = 0; ks < 9; ++ks) {
-      const uint4 lo = *reinterpret_cast<const uint4*>(qrow + 64 * ks + 32 * hh);
-      const uint4 hi = *reinterpret_cast<const uint4*>(qrow + 64 * ks + 32 * hh + 16);
-      qv[ks] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-    }
-#pragma unroll
-    for (int ks = 0; ks < 9; ++ks) asm volatile("" : "+v"(qv[ks]));
-  }
+  load_q128<32, 16>(p, b, head, hh, qv);
   const float c = p.q_scale[0] * p.kv_scale[0] * p.sm_scale * kLog2e;
   const float vscale = p.kv_scale[0];  // the 2^8 carried by P' is folded into the PV scale exponent
 
