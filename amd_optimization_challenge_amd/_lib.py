@@ -39,6 +39,8 @@ SIGNATURES = {
     "mla_absorb_q": (_I, [_P, _P, _P, _I, _I, _P, _P]),
     "mla_v_up_proj": (_I, [_P, _P, _I, _I, _P, _P, _P, _P, _L, _P]),
     "mla_selftest": (_I, [_I, _P, _P, _P]),
+    "mla_decode_fwd_noalloc": (_I, [_P, _P, _L, _P, _L, _P, _L, _P, _P, _P, _I, _I, _I, _F, _I, _P, _P, _P]),
+    "mla_noalloc_scratch_bytes": (_L, []),
 }
 
 

@@ -12,11 +12,10 @@
 
 namespace mla {
 namespace {
-
 thread_local std::string g_last_error;
+}  // namespace
 
-int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
-int fail(int code, const char* fmt, ...) {
+int set_error(int code, const char* fmt, ...) {
   char buf[512];
   va_list ap;
   va_start(ap, fmt);
@@ -26,8 +25,10 @@ int fail(int code, const char* fmt, ...) {
   return code;
 }
 
+namespace {
+
 int hip_fail(hipError_t e, const char* what) {
-  return fail(MLA_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+  return set_error(MLA_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
 }
 
 constexpr int kMaxDevices = 64;
@@ -38,7 +39,7 @@ int cu_count(int* out) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
-  if (dev < 0 || dev >= kMaxDevices) return fail(MLA_ERR_UNSUPPORTED, "device ordinal %d too large", dev);
+  if (dev < 0 || dev >= kMaxDevices) return set_error(MLA_ERR_UNSUPPORTED, "device ordinal %d too large", dev);
   std::lock_guard<std::mutex> lock(g_cu_mutex);
   if (g_cu_count[dev] == 0) {
     int n = 0;
@@ -56,19 +57,19 @@ bool aligned(const void* p, int a) { return (reinterpret_cast<uintptr_t>(p) & (u
 
 int check_qlen(int batch, int q_seq_len) {
   if (q_seq_len < 1 || batch % q_seq_len != 0)
-    return fail(MLA_ERR_INVALID_ARGUMENT, "q_seq_len must be >= 1 and divide the %d query rows (got %d)", batch,
+    return set_error(MLA_ERR_INVALID_ARGUMENT, "q_seq_len must be >= 1 and divide the %d query rows (got %d)", batch,
                 q_seq_len);
   return MLA_OK;
 }
 
 int check_shape(int batch, int num_heads, int kv_mode) {
-  if (batch < 1) return fail(MLA_ERR_INVALID_ARGUMENT, "batch must be >= 1 (got %d)", batch);
+  if (batch < 1) return set_error(MLA_ERR_INVALID_ARGUMENT, "batch must be >= 1 (got %d)", batch);
   if (num_heads != 16 && num_heads != 128)
-    return fail(MLA_ERR_UNSUPPORTED, "num_heads must be 16 or 128 (got %d)", num_heads);
+    return set_error(MLA_ERR_UNSUPPORTED, "num_heads must be 16 or 128 (got %d)", num_heads);
   if (kv_mode < MLA_KV_FP8 || kv_mode > MLA_KV_MXFP4K_FP8V)
-    return fail(MLA_ERR_INVALID_ARGUMENT, "unknown kv_mode %d", kv_mode);
+    return set_error(MLA_ERR_INVALID_ARGUMENT, "unknown kv_mode %d", kv_mode);
   if (num_heads == 128 && kv_mode == MLA_KV_MXFP4)
-    return fail(MLA_ERR_UNSUPPORTED, "kv_mode mxfp4 (fp4 V) is implemented for num_heads=16 only");
+    return set_error(MLA_ERR_UNSUPPORTED, "kv_mode mxfp4 (fp4 V) is implemented for num_heads=16 only");
   return MLA_OK;
 }
 
@@ -128,30 +129,30 @@ int decode_params(const void* q_fp8, const float* q_scale, const void* k_cache, 
   if ((rc = cu_count(&ncu))) return rc;
   *L = workspace_layout(batch, num_heads, kv_mode, ncu);
   if (workspace == nullptr || workspace_bytes < L->total)
-    return fail(MLA_ERR_WORKSPACE_TOO_SMALL, "workspace needs %lld bytes (got %lld)",
+    return set_error(MLA_ERR_WORKSPACE_TOO_SMALL, "workspace needs %lld bytes (got %lld)",
                 (long long)L->total, (long long)workspace_bytes);
-  if (!aligned(workspace, 256)) return fail(MLA_ERR_INVALID_ARGUMENT, "workspace must be 256-byte aligned");
+  if (!aligned(workspace, 256)) return set_error(MLA_ERR_INVALID_ARGUMENT, "workspace must be 256-byte aligned");
   if (!q_fp8 || !q_scale || !k_cache || !kv_indptr || !out)
-    return fail(MLA_ERR_INVALID_ARGUMENT, "null q/q_scale/k_cache/kv_indptr/out pointer");
+    return set_error(MLA_ERR_INVALID_ARGUMENT, "null q/q_scale/k_cache/kv_indptr/out pointer");
   if (!aligned(q_fp8, 16) || !aligned(k_cache, 16) || !aligned(out, 16))
-    return fail(MLA_ERR_INVALID_ARGUMENT, "q, k_cache and out must be 16-byte aligned");
-  if (!(sm_scale > 0.f)) return fail(MLA_ERR_INVALID_ARGUMENT, "sm_scale must be > 0");
+    return set_error(MLA_ERR_INVALID_ARGUMENT, "q, k_cache and out must be 16-byte aligned");
+  if (!(sm_scale > 0.f)) return set_error(MLA_ERR_INVALID_ARGUMENT, "sm_scale must be > 0");
   const bool k_fp4 = kv_mode != MLA_KV_FP8;
   const int64_t krow = k_fp4 ? kFp4RowBytes : kQKDim;
   if (k_row_stride < krow || (k_row_stride % 16) != 0)
-    return fail(MLA_ERR_INVALID_ARGUMENT, "k_row_stride must be >= %lld and a multiple of 16 (got %lld)",
+    return set_error(MLA_ERR_INVALID_ARGUMENT, "k_row_stride must be >= %lld and a multiple of 16 (got %lld)",
                 (long long)krow, (long long)k_row_stride);
   if (k_fp4) {
-    if (!k_scales) return fail(MLA_ERR_INVALID_ARGUMENT, "mxfp4 K needs k_scales");
+    if (!k_scales) return set_error(MLA_ERR_INVALID_ARGUMENT, "mxfp4 K needs k_scales");
     if (k_scale_stride < kMxBlocks)
-      return fail(MLA_ERR_INVALID_ARGUMENT, "k_scale_stride must be >= 18 (got %lld)", (long long)k_scale_stride);
+      return set_error(MLA_ERR_INVALID_ARGUMENT, "k_scale_stride must be >= 18 (got %lld)", (long long)k_scale_stride);
   }
   if (kv_mode == MLA_KV_MXFP4K_FP8V) {
-    if (!v_cache || !aligned(v_cache, 16)) return fail(MLA_ERR_INVALID_ARGUMENT, "fp8 V cache missing or misaligned");
+    if (!v_cache || !aligned(v_cache, 16)) return set_error(MLA_ERR_INVALID_ARGUMENT, "fp8 V cache missing or misaligned");
     if (v_row_stride < kVDim || (v_row_stride % 16) != 0)
-      return fail(MLA_ERR_INVALID_ARGUMENT, "v_row_stride must be >= 512 and a multiple of 16");
+      return set_error(MLA_ERR_INVALID_ARGUMENT, "v_row_stride must be >= 512 and a multiple of 16");
   }
-  if (kv_mode != MLA_KV_MXFP4 && !kv_scale) return fail(MLA_ERR_INVALID_ARGUMENT, "fp8 cache needs kv_scale");
+  if (kv_mode != MLA_KV_MXFP4 && !kv_scale) return set_error(MLA_ERR_INVALID_ARGUMENT, "fp8 cache needs kv_scale");
   char* ws = static_cast<char*>(workspace);
   p->q_fp8 = static_cast<const uint8_t*>(q_fp8);
   p->q_scale = q_scale;
@@ -191,12 +192,12 @@ const char* mla_last_error(void) { return g_last_error.c_str(); }
 int mla_abi_version(void) { return 2; }
 
 int mla_device_cu_count(int* num_cu) {
-  if (!num_cu) return fail(MLA_ERR_INVALID_ARGUMENT, "num_cu is null");
+  if (!num_cu) return set_error(MLA_ERR_INVALID_ARGUMENT, "num_cu is null");
   return cu_count(num_cu);
 }
 
 int mla_workspace_bytes(int batch, int num_heads, int kv_mode, int64_t* bytes) {
-  if (!bytes) return fail(MLA_ERR_INVALID_ARGUMENT, "bytes is null");
+  if (!bytes) return set_error(MLA_ERR_INVALID_ARGUMENT, "bytes is null");
   int rc = check_shape(batch, num_heads, kv_mode);
   if (rc) return rc;
   int ncu = 0;
@@ -207,13 +208,13 @@ int mla_workspace_bytes(int batch, int num_heads, int kv_mode, int64_t* bytes) {
 
 int mla_quant_fp8_per_tensor(const void* x_bf16, int64_t n, void* out_fp8, float* out_scale,
                              void* workspace, int64_t workspace_bytes, void* stream) {
-  if (n < 1) return fail(MLA_ERR_INVALID_ARGUMENT, "n must be >= 1");
+  if (n < 1) return set_error(MLA_ERR_INVALID_ARGUMENT, "n must be >= 1");
   if (!x_bf16 || !out_fp8 || !out_scale || !workspace)
-    return fail(MLA_ERR_INVALID_ARGUMENT, "null pointer argument");
+    return set_error(MLA_ERR_INVALID_ARGUMENT, "null pointer argument");
   if (!aligned(x_bf16, 16) || !aligned(out_fp8, 8) || !aligned(workspace, 16))
-    return fail(MLA_ERR_INVALID_ARGUMENT, "x must be 16-byte, out 8-byte, workspace 16-byte aligned");
+    return set_error(MLA_ERR_INVALID_ARGUMENT, "x must be 16-byte, out 8-byte, workspace 16-byte aligned");
   if (workspace_bytes < kQuantScratchBytes)
-    return fail(MLA_ERR_WORKSPACE_TOO_SMALL, "workspace needs %lld bytes", (long long)kQuantScratchBytes);
+    return set_error(MLA_ERR_WORKSPACE_TOO_SMALL, "workspace needs %lld bytes", (long long)kQuantScratchBytes);
   hipStream_t s = static_cast<hipStream_t>(stream);
   uint32_t* partials = static_cast<uint32_t*>(workspace);
   int nb = 0;
@@ -229,15 +230,15 @@ int mla_quant_fp8_per_tensor(const void* x_bf16, int64_t n, void* out_fp8, float
 int mla_pack_mxfp4(const void* x_bf16, int64_t rows, int cols, int64_t x_row_stride, void* packed,
                    int64_t packed_row_stride, void* scales, int64_t scale_row_stride, void* stream) {
   if (rows < 0 || cols < 32 || (cols % 32) != 0)
-    return fail(MLA_ERR_INVALID_ARGUMENT, "cols must be a positive multiple of 32 (got %d)", cols);
+    return set_error(MLA_ERR_INVALID_ARGUMENT, "cols must be a positive multiple of 32 (got %d)", cols);
   if (rows == 0) return MLA_OK;
-  if (!x_bf16 || !packed || !scales) return fail(MLA_ERR_INVALID_ARGUMENT, "null pointer argument");
+  if (!x_bf16 || !packed || !scales) return set_error(MLA_ERR_INVALID_ARGUMENT, "null pointer argument");
   if (x_row_stride < 2LL * cols || (x_row_stride % 16) != 0 || !aligned(x_bf16, 16))
-    return fail(MLA_ERR_INVALID_ARGUMENT, "x rows must be 16-byte aligned with stride >= 2*cols");
+    return set_error(MLA_ERR_INVALID_ARGUMENT, "x rows must be 16-byte aligned with stride >= 2*cols");
   if (packed_row_stride < cols / 2 || (packed_row_stride % 16) != 0 || !aligned(packed, 16))
-    return fail(MLA_ERR_INVALID_ARGUMENT, "packed rows must be 16-byte aligned with stride >= cols/2");
+    return set_error(MLA_ERR_INVALID_ARGUMENT, "packed rows must be 16-byte aligned with stride >= cols/2");
   if (scale_row_stride < cols / 32)
-    return fail(MLA_ERR_INVALID_ARGUMENT, "scale_row_stride must be >= cols/32");
+    return set_error(MLA_ERR_INVALID_ARGUMENT, "scale_row_stride must be >= cols/32");
   hipError_t e = launch_pack_mxfp4(static_cast<const uint16_t*>(x_bf16), rows, cols, x_row_stride,
                                    static_cast<uint8_t*>(packed), packed_row_stride,
                                    static_cast<uint8_t*>(scales), scale_row_stride,
@@ -251,24 +252,24 @@ int mla_append_kv(const void* x_bf16, int64_t n, int64_t x_row_stride, const int
                   int64_t fp4_row_stride, void* fp4_scales, int64_t fp4_scale_stride, uint32_t* amax_out,
                   void* stream) {
   if (n < 0 || n > kAppendMaxTokens)
-    return fail(MLA_ERR_INVALID_ARGUMENT, "n must be in [0, %lld] (got %lld)", (long long)kAppendMaxTokens,
+    return set_error(MLA_ERR_INVALID_ARGUMENT, "n must be in [0, %lld] (got %lld)", (long long)kAppendMaxTokens,
                 (long long)n);
-  if (!fp8_cache && !fp4_cache) return fail(MLA_ERR_INVALID_ARGUMENT, "no cache to write (both NULL)");
+  if (!fp8_cache && !fp4_cache) return set_error(MLA_ERR_INVALID_ARGUMENT, "no cache to write (both NULL)");
   if (n == 0) return MLA_OK;
-  if (!x_bf16) return fail(MLA_ERR_INVALID_ARGUMENT, "null pointer argument");
+  if (!x_bf16) return set_error(MLA_ERR_INVALID_ARGUMENT, "null pointer argument");
   if (x_row_stride < 2LL * kQKDim || (x_row_stride % 16) != 0 || !aligned(x_bf16, 16))
-    return fail(MLA_ERR_INVALID_ARGUMENT, "x rows must be 16-byte aligned with stride >= 1152 bytes");
+    return set_error(MLA_ERR_INVALID_ARGUMENT, "x rows must be 16-byte aligned with stride >= 1152 bytes");
   if (fp8_cache) {
-    if (!fp8_scale) return fail(MLA_ERR_INVALID_ARGUMENT, "fp8_cache needs fp8_scale");
+    if (!fp8_scale) return set_error(MLA_ERR_INVALID_ARGUMENT, "fp8_cache needs fp8_scale");
     if (fp8_row_stride < kQKDim || (fp8_row_stride % 16) != 0 || !aligned(fp8_cache, 16))
-      return fail(MLA_ERR_INVALID_ARGUMENT, "fp8 cache rows must be 16-byte aligned with stride >= 576");
+      return set_error(MLA_ERR_INVALID_ARGUMENT, "fp8 cache rows must be 16-byte aligned with stride >= 576");
   }
   if (fp4_cache) {
-    if (!fp4_scales) return fail(MLA_ERR_INVALID_ARGUMENT, "fp4_cache needs fp4_scales");
+    if (!fp4_scales) return set_error(MLA_ERR_INVALID_ARGUMENT, "fp4_cache needs fp4_scales");
     if (fp4_row_stride < kFp4RowBytes || (fp4_row_stride % 16) != 0 || !aligned(fp4_cache, 16))
-      return fail(MLA_ERR_INVALID_ARGUMENT, "mxfp4 cache rows must be 16-byte aligned with stride >= 288");
+      return set_error(MLA_ERR_INVALID_ARGUMENT, "mxfp4 cache rows must be 16-byte aligned with stride >= 288");
     if (fp4_scale_stride < kMxBlocks)
-      return fail(MLA_ERR_INVALID_ARGUMENT, "fp4_scale_stride must be >= 18");
+      return set_error(MLA_ERR_INVALID_ARGUMENT, "fp4_scale_stride must be >= 18");
   }
   hipError_t e = launch_append_kv(static_cast<const uint16_t*>(x_bf16), n, x_row_stride, slots,
                                   static_cast<uint8_t*>(fp8_cache), fp8_row_stride, fp8_scale,
@@ -284,13 +285,13 @@ int mla_plan(const int32_t* kv_indptr, int batch, int q_seq_len, int num_heads, 
   int rc = check_shape(batch, num_heads, kv_mode);
   if (rc) return rc;
   if ((rc = check_qlen(batch, q_seq_len))) return rc;
-  if (!kv_indptr || !workspace) return fail(MLA_ERR_INVALID_ARGUMENT, "null pointer argument");
-  if (!aligned(workspace, 256)) return fail(MLA_ERR_INVALID_ARGUMENT, "workspace must be 256-byte aligned");
+  if (!kv_indptr || !workspace) return set_error(MLA_ERR_INVALID_ARGUMENT, "null pointer argument");
+  if (!aligned(workspace, 256)) return set_error(MLA_ERR_INVALID_ARGUMENT, "workspace must be 256-byte aligned");
   int ncu = 0;
   if ((rc = cu_count(&ncu))) return rc;
   WsLayout L = workspace_layout(batch, num_heads, kv_mode, ncu);
   if (workspace_bytes < L.total)
-    return fail(MLA_ERR_WORKSPACE_TOO_SMALL, "workspace needs %lld bytes (got %lld)", (long long)L.total,
+    return set_error(MLA_ERR_WORKSPACE_TOO_SMALL, "workspace needs %lld bytes (got %lld)", (long long)L.total,
                 (long long)workspace_bytes);
   int32_t* plan = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + L.plan_off);
   hipError_t e = launch_plan(kv_indptr, batch, q_seq_len, target_items_for(batch, num_heads, kv_mode, ncu),
@@ -320,12 +321,12 @@ int mla_combine(int batch, int num_heads, void* workspace, int64_t workspace_byt
                 float* lse_out, void* stream) {
   int rc = check_shape(batch, num_heads, MLA_KV_FP8);
   if (rc) return rc;
-  if (!workspace || !out_bf16) return fail(MLA_ERR_INVALID_ARGUMENT, "null pointer argument");
+  if (!workspace || !out_bf16) return set_error(MLA_ERR_INVALID_ARGUMENT, "null pointer argument");
   int ncu = 0;
   if ((rc = cu_count(&ncu))) return rc;
   WsLayout L = workspace_layout(batch, num_heads, MLA_KV_FP8, ncu);
   if (workspace_bytes < L.total)
-    return fail(MLA_ERR_WORKSPACE_TOO_SMALL, "workspace needs %lld bytes (got %lld)", (long long)L.total,
+    return set_error(MLA_ERR_WORKSPACE_TOO_SMALL, "workspace needs %lld bytes (got %lld)", (long long)L.total,
                 (long long)workspace_bytes);
   char* ws = static_cast<char*>(workspace);
   DecodeParams p = {};
@@ -347,8 +348,8 @@ int mla_decode_fwd(const void* q_bf16, const void* k_cache, int64_t k_row_stride
                    const float* kv_scale, const int32_t* kv_indptr, const int32_t* kv_indices, int batch,
                    int q_seq_len, int num_heads, float sm_scale, int kv_mode, void* workspace,
                    int64_t workspace_bytes, void* out_bf16, float* lse_out, void* stream) {
-  if (!q_bf16 || !aligned(q_bf16, 16)) return fail(MLA_ERR_INVALID_ARGUMENT, "q must be non-null and 16-byte aligned");
-  if (!workspace) return fail(MLA_ERR_INVALID_ARGUMENT, "null workspace");
+  if (!q_bf16 || !aligned(q_bf16, 16)) return set_error(MLA_ERR_INVALID_ARGUMENT, "q must be non-null and 16-byte aligned");
+  if (!workspace) return set_error(MLA_ERR_INVALID_ARGUMENT, "null workspace");
   char* ws = static_cast<char*>(workspace);
   int rc = check_shape(batch, num_heads, kv_mode);
   if (rc) return rc;
@@ -357,7 +358,7 @@ int mla_decode_fwd(const void* q_bf16, const void* k_cache, int64_t k_row_stride
   if ((rc = cu_count(&ncu))) return rc;
   WsLayout L0 = workspace_layout(batch, num_heads, kv_mode, ncu);
   if (workspace_bytes < L0.total)
-    return fail(MLA_ERR_WORKSPACE_TOO_SMALL, "workspace needs %lld bytes (got %lld)", (long long)L0.total,
+    return set_error(MLA_ERR_WORKSPACE_TOO_SMALL, "workspace needs %lld bytes (got %lld)", (long long)L0.total,
                 (long long)workspace_bytes);
   uint8_t* q_fp8 = reinterpret_cast<uint8_t*>(ws + L0.qfp8_off);
   float* q_scale = reinterpret_cast<float*>(ws + L0.quant_off + 4096);
@@ -395,11 +396,11 @@ int mla_decode_fwd(const void* q_bf16, const void* k_cache, int64_t k_row_stride
 int mla_absorb_q(const void* q_nope, const void* q_rope, const void* w_uk, int batch, int num_heads,
                  void* q_out, void* stream) {
   if (batch < 1 || num_heads < 1 || num_heads > 65535)
-    return fail(MLA_ERR_INVALID_ARGUMENT, "batch must be >= 1 and num_heads in [1, 65535] (got %d, %d)", batch,
+    return set_error(MLA_ERR_INVALID_ARGUMENT, "batch must be >= 1 and num_heads in [1, 65535] (got %d, %d)", batch,
                 num_heads);
-  if (!q_nope || !q_rope || !w_uk || !q_out) return fail(MLA_ERR_INVALID_ARGUMENT, "null pointer argument");
+  if (!q_nope || !q_rope || !w_uk || !q_out) return set_error(MLA_ERR_INVALID_ARGUMENT, "null pointer argument");
   if (!aligned(q_nope, 16) || !aligned(q_rope, 16) || !aligned(w_uk, 16) || !aligned(q_out, 16))
-    return fail(MLA_ERR_INVALID_ARGUMENT, "q_nope, q_rope, w_uk and q_out must be 16-byte aligned");
+    return set_error(MLA_ERR_INVALID_ARGUMENT, "q_nope, q_rope, w_uk and q_out must be 16-byte aligned");
   hipError_t e = launch_absorb_q(static_cast<const uint16_t*>(q_nope), static_cast<const uint16_t*>(q_rope),
                                  static_cast<const uint16_t*>(w_uk), batch, num_heads,
                                  static_cast<uint16_t*>(q_out), static_cast<hipStream_t>(stream));
@@ -410,18 +411,18 @@ int mla_absorb_q(const void* q_nope, const void* q_rope, const void* w_uk, int b
 int mla_v_up_proj(const void* o, const void* w_uv, int batch, int num_heads, void* y_bf16, void* out_fp8,
                   float* out_scale, void* workspace, int64_t workspace_bytes, void* stream) {
   if (batch < 1 || num_heads < 1 || num_heads > kUpProjMaxHeads)
-    return fail(MLA_ERR_INVALID_ARGUMENT, "batch must be >= 1 and num_heads in [1, %d] (got %d, %d)",
+    return set_error(MLA_ERR_INVALID_ARGUMENT, "batch must be >= 1 and num_heads in [1, %d] (got %d, %d)",
                 kUpProjMaxHeads, batch, num_heads);
-  if (!o || !w_uv || !y_bf16) return fail(MLA_ERR_INVALID_ARGUMENT, "null pointer argument");
+  if (!o || !w_uv || !y_bf16) return set_error(MLA_ERR_INVALID_ARGUMENT, "null pointer argument");
   if (!aligned(o, 16) || !aligned(w_uv, 16) || !aligned(y_bf16, 16))
-    return fail(MLA_ERR_INVALID_ARGUMENT, "o, w_uv and y must be 16-byte aligned");
+    return set_error(MLA_ERR_INVALID_ARGUMENT, "o, w_uv and y must be 16-byte aligned");
   const bool fp8 = out_fp8 != nullptr;
   if (fp8) {
-    if (!out_scale || !workspace) return fail(MLA_ERR_INVALID_ARGUMENT, "the fp8 output needs out_scale and workspace");
+    if (!out_scale || !workspace) return set_error(MLA_ERR_INVALID_ARGUMENT, "the fp8 output needs out_scale and workspace");
     if (!aligned(out_fp8, 8) || !aligned(workspace, 16))
-      return fail(MLA_ERR_INVALID_ARGUMENT, "out_fp8 must be 8-byte and workspace 16-byte aligned");
+      return set_error(MLA_ERR_INVALID_ARGUMENT, "out_fp8 must be 8-byte and workspace 16-byte aligned");
     if (workspace_bytes < kQuantScratchBytes)
-      return fail(MLA_ERR_WORKSPACE_TOO_SMALL, "workspace needs %lld bytes", (long long)kQuantScratchBytes);
+      return set_error(MLA_ERR_WORKSPACE_TOO_SMALL, "workspace needs %lld bytes", (long long)kQuantScratchBytes);
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
   uint32_t* partials = fp8 ? static_cast<uint32_t*>(workspace) : nullptr;
@@ -438,9 +439,9 @@ int mla_v_up_proj(const void* o, const void* w_uv, int batch, int num_heads, voi
 }
 
 int mla_selftest(int which, const void* in, void* out, void* stream) {
-  if (!in || !out) return fail(MLA_ERR_INVALID_ARGUMENT, "null pointer argument");
+  if (!in || !out) return set_error(MLA_ERR_INVALID_ARGUMENT, "null pointer argument");
   hipError_t e = launch_selftest(which, in, out, static_cast<hipStream_t>(stream));
-  if (e == hipErrorInvalidValue) return fail(MLA_ERR_INVALID_ARGUMENT, "unknown selftest %d", which);
+  if (e == hipErrorInvalidValue) return set_error(MLA_ERR_INVALID_ARGUMENT, "unknown selftest %d", which);
   if (e != hipSuccess) return hip_fail(e, "selftest launch");
   return MLA_OK;
 }

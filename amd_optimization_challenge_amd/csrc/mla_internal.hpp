@@ -14,6 +14,11 @@ constexpr int kAmaxMaxBlocks = 1024;
 constexpr int64_t kAppendMaxTokens = (1LL << 31) / (kQKDim / 8);
 // Byte size of the quantizer scratch area at the front of every workspace.
 constexpr int64_t kQuantScratchBytes = 8192;
+// Device scratch of mla_decode_fwd_noalloc (per device, held until exit).
+constexpr int64_t kNoAllocScratchBytes = 64LL << 20;
+
+// Records the thread's last error message (mla_last_error) and returns code.
+int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 
 // Workspace carve-up for one decode call; every offset is 256-byte aligned.
 struct WsLayout {

@@ -265,6 +265,32 @@ def decode_fwd(q, kv_data, kv_indptr, kv_indices, sm_scale, kv_mode="fp8", out=N
     return (out, lse) if return_lse else out
 
 
+def decode_fwd_noalloc(q, kv_data, kv_indptr, kv_indices, sm_scale, kv_mode="fp8", out=None, q_seq_len=1,
+                       return_lse=False):
+    """``decode_fwd`` through ``mla_decode_fwd_noalloc``: the library's own
+    per-device scratch array replaces the workspace, so nothing but ``out``
+    (and the lse, when asked for) is allocated here -- pass ``out`` to allocate
+    nothing.  Calls that overlap on one device race on that array."""
+    _require_cuda(q, kv_indptr, kv_indices, out)
+    if q.dtype != torch.bfloat16 or q.dim() != 3 or q.shape[-1] != QK_DIM or not q.is_contiguous():
+        raise ValueError("q must be contiguous bf16 [rows, heads, 576]")
+    batch, num_heads = q.shape[0], q.shape[1]
+    q_seq_len = int(q_seq_len)
+    if q_seq_len < 1 or batch % q_seq_len != 0 or kv_indptr.numel() != batch // q_seq_len + 1:
+        raise ValueError("query rows, q_seq_len and kv_indptr do not fit")
+    mode = kv_mode_id(kv_mode)
+    k, ks, ksc, kss, v, vs, sc = _kv_args(mode, kv_data)
+    if out is None:
+        out = torch.empty((batch, num_heads, V_DIM), dtype=torch.bfloat16, device=q.device)
+    lse = torch.empty((batch, num_heads), dtype=torch.float32, device=q.device) if return_lse else None
+    with torch.cuda.device(q.device):
+        _lib.check(_lib.load().mla_decode_fwd_noalloc(
+            _ptr(q), _ptr(k), ks, _ptr(ksc), kss, _ptr(v), vs, _ptr(sc), _ptr(kv_indptr), _ptr(kv_indices),
+            batch, q_seq_len, num_heads, float(sm_scale), mode, _ptr(out), _ptr(lse), _stream()),
+            "mla_decode_fwd_noalloc")
+    return (out, lse) if return_lse else out
+
+
 def selftest(which: int, inp: torch.Tensor, out: torch.Tensor) -> None:
     with torch.cuda.device(inp.device):
         _lib.check(_lib.load().mla_selftest(which, _ptr(inp), _ptr(out), _stream()), "mla_selftest")

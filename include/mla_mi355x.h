@@ -186,6 +186,28 @@ int mla_decode_fwd(const void* q_bf16, const void* k_cache, int64_t k_row_stride
                    int64_t workspace_bytes, void* out_bf16, float* lse_out, void* stream);
 
 /*
+ * mla_decode_fwd without a caller workspace, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  No counterpart in the reference.  Arguments mean what
+ * they mean for mla_decode_fwd; the workspace is instead a device array inside
+ * the library of mla_noalloc_scratch_bytes() = 64 MiB per device (held from
+ * the first call on a device until the process ends).  A shape whose
+ * mla_workspace_bytes exceeds it returns MLA_ERR_WORKSPACE_TOO_SMALL.  Calls
+ * on one device share that array: calls that overlap on a device (other
+ * streams, other threads) race; calls ordered on one stream do not.  It calls
+ * no allocator.
+ */
+int mla_decode_fwd_noalloc(const void* q_bf16, const void* k_cache, int64_t k_row_stride,
+                           const void* k_scales, int64_t k_scale_stride, const void* v_cache,
+                           int64_t v_row_stride, const float* kv_scale,
+                           const int32_t* kv_indptr, const int32_t* kv_indices, int batch,
+                           int q_seq_len, int num_heads, float sm_scale, int kv_mode,
+                           void* out_bf16, float* lse_out, void* stream);
+
+/* Size in bytes of mla_decode_fwd_noalloc's per-device scratch array. */
+int64_t mla_noalloc_scratch_bytes(void);
+
+/*
  * Diagnostics (no counterpart in the reference): runs one wave of a built-in
  * check that pins an MFMA operand/accumulator layout or a conversion the
  * kernels rely on.  `in`/`out` are small device buffers whose layout per

@@ -13,7 +13,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 def declared_symbols():
     text = open(os.path.join(ROOT, "include", "mla_mi355x.h")).read()
-    return sorted(set(re.findall(r"^\s*(?:const\s+char\s*\*|int)\s+(mla_\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:const\s+char\s*\*|int64_t|int)\s+(mla_\w+)\s*\(", text, re.M)))
 
 
 def test_header_and_binding_agree():
@@ -66,6 +66,10 @@ def test_argument_errors_without_device():
     assert lib.mla_plan(None, 6, 4, 16, 0, None, 0, None) == _lib.MLA_ERR_INVALID_ARGUMENT
     assert lib.mla_decode_fwd(None, None, 576, None, 0, None, 0, None, None, None, 6, 4, 16, 0.1, 0, None, 0,
                               None, None, None) == _lib.MLA_ERR_INVALID_ARGUMENT
+    # the no-alloc variant: stated scratch size, shape errors before any device call
+    assert lib.mla_noalloc_scratch_bytes() == 64 << 20
+    assert lib.mla_decode_fwd_noalloc(None, None, 576, None, 0, None, 0, None, None, None, 4, 1, 24, 0.1, 0,
+                                      None, None, None) == _lib.MLA_ERR_UNSUPPORTED
 
 
 def test_custom_kernel_rejects_unsupported_configs_before_launch():
