@@ -1,6 +1,7 @@
 """Benchmark of the MLA absorbed-decode operator on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--config C] [--no-cpu] [--only-headline]
+    python bench.py [--steps K] [--warmup W] [--config C] [--no-cpu] [--no-probe] [--only-headline]
+    python bench.py --gather-probe      # gather-ceiling sweep (own JSON line)
 
 Prints ONE JSON line.  ``value`` is the mean device time of one
 ``custom_kernel(data)`` call (Q quant + plan + decode + combine) in µs for the
@@ -15,7 +16,11 @@ back-to-back launches over rotating copies of the cache that evict each other
 from L2/MALL, one pair of events around them) by its algorithmic bytes:
 T*(c_kv+4) KV + index bytes, the fp8 Q read and the bf16 output write.  ``cpu_baseline`` times the
 CPU oracle (the reference path restated: quantize Q, dequantize, fp32
-attention) on this host, on a bounded sample of the same workload.
+attention) on this host for every config (the whole config when it fits the
+per-config budget, else its leading sequences, scaled by token share).  Each
+config also carries the gather ceiling of its cache layout: the
+mla_probe_gather variants (the decode's KV gather with no compute) over the
+same rows, and the decode's fraction of it.
 """
 from __future__ import annotations
 
@@ -39,19 +44,40 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
+def source_digest():
+    """First 16 hex digits of the SHA-256 over the library's HIP sources (name +
+    bytes, sorted): identifies the kernels a counter profile was taken on."""
+    import hashlib
+
+    d = hashlib.sha256()
+    csrc = os.path.join(ROOT, "amd_optimization_challenge_amd", "csrc")
+    for name in sorted(os.listdir(csrc)):
+        if name.endswith((".hip", ".hpp")):
+            d.update(name.encode())
+            with open(os.path.join(csrc, name), "rb") as f:
+                d.update(f.read())
+    return d.hexdigest()[:16]
+
+
 def measured_traffic(cid):
     """HBM bytes per decode launch from the committed counter summary
     (profiles/decode_hbm_traffic.md: FETCH_SIZE and WRITE_SIZE passes scaled by
-    a 256 MiB copy); None when the summary has no figure for this config."""
+    a 256 MiB copy) and the source digest it was taken on.  The figure is
+    returned only when that digest equals the current sources' (else None: the
+    profile belongs to other kernels)."""
     path = os.path.join(ROOT, "profiles", "decode_hbm_traffic.md")
+    fig, src = None, None
     try:
         with open(path) as f:
             for line in f:
                 if line.startswith(f"traffic.config{cid}="):
-                    return int(line.split("=", 1)[1])
+                    fig = int(line.split("=", 1)[1])
+                elif line.startswith("source_digest="):
+                    src = line.split("=", 1)[1].strip()
     except OSError:
-        return None
-    return None
+        return None, None
+    cur = source_digest()
+    return (fig if src == cur else None), src
 
 
 def algorithmic(cfg, T):
@@ -63,7 +89,96 @@ def algorithmic(cfg, T):
     return call_bytes, decode_bytes, flops
 
 
-def time_config(cid, steps, warmup, flush_buf):
+# Gather-probe variants per cache layout (mla_probe_gather): (method, waves,
+# stages, work-groups per CU).  Layout 0 = fp8 576-B rows, 1 = fp4 288-B rows +
+# 18 scale bytes, 2 = layout 1 + fp8 512-B V rows.
+PROBE_VARIANTS = {
+    0: [(0, 4, 4, 1), (0, 4, 3, 1), (0, 4, 2, 2), (0, 8, 4, 1), (0, 8, 2, 2), (2, 4, 0, 1), (2, 4, 0, 2),
+        (2, 8, 0, 1), (2, 8, 0, 2)],
+    1: [(0, 4, 4, 1), (0, 4, 3, 2), (0, 8, 4, 1), (1, 4, 3, 2)],
+    2: [(0, 4, 2, 1), (0, 8, 2, 1), (1, 4, 2, 1)],
+}
+PROBE_METHODS = {0: "lds-dma, dword scale DMAs", 1: "lds-dma, one-byte scale DMAs", 2: "register loads",
+                 3: "contiguous stream"}
+LAYOUT_OF_MODE = {"fp8": 0, "mxfp4": 1, "mxfp4k_fp8v": 2}
+# bytes the gather moves per token, by layout (index word included)
+GATHER_BYTES = {0: 576 + 4, 1: 306 + 4, 2: 818 + 4}
+
+
+def probe_gather(layout, method, waves, stages, groups, caches, idx, ntok, sink):
+    """One mla_probe_gather launch on torch's current stream.  caches = (rows,
+    row_stride, scales, scale_stride, vrows, v_stride)."""
+    from amd_optimization_challenge_amd import _lib, ops
+
+    rows, rs, sc, ss, vr, vs = caches
+    _lib.check(_lib.load().mla_probe_gather(layout, method, waves, stages, groups, ops._ptr(rows), rs,
+                                            ops._ptr(sc), ss, ops._ptr(vr), vs, ops._ptr(idx), ntok,
+                                            ops._ptr(sink), ops._stream()), "mla_probe_gather")
+
+
+def time_probe(variant, layout, copies, idx, ntok, reps):
+    """Mean µs per launch of one probe variant: `reps` back-to-back launches over
+    rotating cache copies (each launch reads a copy the others evicted)."""
+    import torch
+
+    from amd_optimization_challenge_amd import ops
+
+    method, waves, stages, gpc = variant
+    groups = gpc * ops.cu_count()
+    sink = torch.empty(1024, dtype=torch.uint8, device="cuda")
+    for c in copies:
+        probe_gather(layout, method, waves, stages, groups, c, idx, ntok, sink)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for i in range(reps):
+        probe_gather(layout, method, waves, stages, groups, copies[i % len(copies)], idx, ntok, sink)
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / reps
+
+
+def probe_caches(kv_copy, mode):
+    """(rows, row_stride, scales, scale_stride, vrows, v_stride) of one cache copy
+    for the probe's layout of `mode` (scales padded by one row: the dword scale
+    DMAs may read up to 8 bytes past the last row's 18)."""
+    from amd_optimization_challenge_amd import ops
+
+    if mode == "fp8":
+        k = ops.as_bytes(kv_copy["fp8"][0]).reshape(kv_copy["fp8"][0].shape[0], -1)
+        return (k, k.stride(0), None, 0, None, 0)
+    f4 = ops.as_bytes(kv_copy["mxfp4"][0]).reshape(kv_copy["mxfp4"][0].shape[0], -1)
+    sc = kv_copy["mxfp4_scales_padded"]
+    if mode == "mxfp4":
+        return (f4, f4.stride(0), sc, sc.stride(0), None, 0)
+    v = ops.as_bytes(kv_copy["fp8"][0]).reshape(kv_copy["fp8"][0].shape[0], -1)
+    return (f4, f4.stride(0), sc, sc.stride(0), v, v.stride(0))
+
+
+def make_copies(kv_data, ncopy):
+    """Device copies of the quantized caches (what the decode reads); mxfp4
+    scale copies sit in a buffer one row longer (the probe's read slack)."""
+    import torch
+
+    copies = []
+    for _ in range(ncopy):
+        c = {}
+        for k, v in kv_data.items():
+            if k == "bf16":
+                continue
+            if k == "mxfp4":
+                sc = v[1]
+                pad = torch.empty((sc.shape[0] + 1, sc.shape[1]), dtype=sc.dtype, device=sc.device)
+                pad[: sc.shape[0]].copy_(sc)
+                c[k] = (v[0].clone(), pad[: sc.shape[0]])
+                c["mxfp4_scales_padded"] = pad.view(torch.uint8)
+            else:
+                c[k] = tuple(t.clone() for t in v)
+        copies.append(c)
+    return copies
+
+
+def time_config(cid, steps, warmup, flush_buf, probe=True):
     import torch
 
     from amd_optimization_challenge_amd import custom_kernel, inputs, ops
@@ -104,7 +219,7 @@ def time_config(cid, steps, warmup, flush_buf):
     quantized = {k: v for k, v in kv_data.items() if k != "bf16"}  # what the decode reads
     cache_bytes = sum(t.numel() * t.element_size() for v in quantized.values() for t in v)
     ncopy = min(64, max(2, -(-(512 << 20) // cache_bytes) + 1))  # config 1's 0.6 MB cache stays warm
-    copies = [{k: tuple(t.clone() for t in v) for k, v in quantized.items()} for _ in range(ncopy)]
+    copies = make_copies(kv_data, ncopy)
     args = (kv_indptr, cfg["kv_indices"], H, cfg["sm_scale"], mode, ws, out)
     for i in range(ncopy):  # warm-up: every copy once
         ops.decode(qf8, qsc, copies[i], *args)
@@ -117,6 +232,23 @@ def time_config(cid, steps, warmup, flush_buf):
     ops.combine(B, H, ws, out)
     torch.cuda.synchronize()
     dec_us = [e0.elapsed_time(e1) * 1e3 / steps]
+
+    # the gather ceiling of this config: the probe's variants for its cache
+    # layout over the same rows (kv_indices, whole 64-token tiles), same copies
+    gather = None
+    T64 = (T // 64) * 64
+    if probe and T64 >= 64:
+        layout = LAYOUT_OF_MODE[mode]
+        pc = [probe_caches(c, mode) for c in copies]
+        best = None
+        for var in PROBE_VARIANTS[layout]:
+            us = time_probe(var, layout, pc, cfg["kv_indices"], T64, max(steps, 10)) * T / T64
+            if best is None or us < best[0]:
+                best = (us, var)
+        us, var = best
+        gbs = T * GATHER_BYTES[layout] / (us * 1e-6) / 1e9
+        gather = {"us": round(us, 3), "GBs": round(gbs, 1), "variant": {
+            "method": PROBE_METHODS[var[0]], "waves": var[1], "stages": var[2], "groups_per_cu": var[3]}}
     del copies
     ref = custom_kernel(data)
     torch.cuda.synchronize()
@@ -136,13 +268,53 @@ def time_config(cid, steps, warmup, flush_buf):
         "bytes_alg_call": call_bytes, "bytes_alg_decode": dec_bytes, "flops_alg": flops,
         "wall_s": round(wall, 4),
     }
+    if gather is not None:
+        res["gather_ceiling"] = gather
+        res["frac_of_gather_ceiling"] = round(gather["us"] / dec_mean, 4)
     log(f"[bench] config {cid}: {res['us_per_call_mean']} us/call, decode {res['us_decode_kernel_mean']} us "
-        f"({res['decode_hbm_GBs']} GB/s, {100 * res['decode_hbm_frac']:.1f}% HBM)")
+        f"({res['decode_hbm_GBs']} GB/s, {100 * res['decode_hbm_frac']:.1f}% HBM)"
+        + (f", gather ceiling {gather['us']} us ({gather['GBs']} GB/s)" if gather else ""))
     return res, data
 
 
+def gather_probe_sweep(reps, ntok=1 << 20):
+    """Every probe variant on synthetic caches of `ntok` tokens (random bytes),
+    with random-permutation and contiguous kv_indices, plus the contiguous
+    stream: the gather ceilings behind the decode kernels' HBM rates."""
+    import torch
+
+    from amd_optimization_challenge_amd import ops
+
+    g = torch.Generator(device="cuda").manual_seed(3)
+    f8 = torch.randint(0, 256, (ntok, 576), dtype=torch.uint8, device="cuda", generator=g)
+    f4 = torch.randint(0, 256, (ntok, 288), dtype=torch.uint8, device="cuda", generator=g)
+    scp = torch.randint(100, 140, (ntok + 1, 18), dtype=torch.uint8, device="cuda", generator=g)
+    layouts = {0: (f8, 576, None, 0, None, 0), 1: (f4, 288, scp, 18, None, 0), 2: (f4, 288, scp, 18, f8, 576)}
+    idxs = {"random": torch.randperm(ntok, device="cuda", generator=g).to(torch.int32),
+            "contiguous": torch.arange(ntok, dtype=torch.int32, device="cuda")}
+    out = []
+    for layout, caches in layouts.items():
+        for order, idx in idxs.items():
+            for var in PROBE_VARIANTS[layout]:
+                us = time_probe(var, layout, [caches], idx, ntok, reps)
+                gbs = ntok * GATHER_BYTES[layout] / (us * 1e-6) / 1e9
+                out.append({"layout": layout, "order": order, "method": PROBE_METHODS[var[0]], "waves": var[1],
+                            "stages": var[2], "groups_per_cu": var[3], "us": round(us, 2), "GBs": round(gbs, 1)})
+                log(f"[probe] layout {layout} {order:10s} {PROBE_METHODS[var[0]]:28s} w{var[1]} s{var[2]} "
+                    f"g{var[3]}: {us:8.2f} us {gbs:7.1f} GB/s")
+    for gpc in (1, 2, 4, 8):  # plain stream of the fp8 cache bytes
+        us = time_probe((3, 4, 0, gpc), 0, [layouts[0]], None, ntok, reps)
+        gbs = ntok * 576 / (us * 1e-6) / 1e9
+        out.append({"layout": 0, "order": "stream", "method": PROBE_METHODS[3], "waves": 4, "stages": 0,
+                    "groups_per_cu": gpc, "us": round(us, 2), "GBs": round(gbs, 1)})
+        log(f"[probe] stream {gpc} groups/CU: {us:8.2f} us {gbs:7.1f} GB/s")
+    return {"metric": "gather ceiling: GB/s of gathered cache bytes (+4 B index per token), no compute",
+            "tokens": ntok, "reps": reps, "cu_count": ops.cu_count(), "results": out}
+
+
 def cpu_baseline(cid, data, budget_s):
-    """Oracle reference path on this host's CPU over a bounded sample of sequences."""
+    """Oracle reference path on this host's CPU: the whole config when one run
+    fits the budget, else the leading sequences that do (scaled by token share)."""
     import numpy as np
     import torch
 
@@ -154,39 +326,49 @@ def cpu_baseline(cid, data, budget_s):
     idx = cfg["kv_indices"].cpu().numpy()
     B = q.shape[0]
     T = int(indptr[-1])
-    # sample: leading sequences holding about 1/8 of the tokens (at least one)
-    nb = 1
-    while nb < B and indptr[nb] < T / 8:
-        nb += 1
-    sub_ptr = indptr[: nb + 1]
-    rows = idx[: sub_ptr[-1]]
-    caches = {}
-    if "fp8" in kv_data:
-        caches.update(fp8_codes=kv_data["fp8"][0].view(torch.uint8).reshape(-1, 576).cpu().numpy()[rows],
-                      fp8_scale=np.float32(kv_data["fp8"][1].item()))
-    if "mxfp4" in kv_data:
-        caches.update(fp4_packed=kv_data["mxfp4"][0].view(torch.uint8).reshape(-1, 288).cpu().numpy()[rows],
-                      fp4_scales=kv_data["mxfp4"][1].view(torch.uint8).cpu().numpy()[rows])
-    qb = O.bf16_tensor_bits(q[:nb])
-    local_idx = np.arange(sub_ptr[-1])
+    f8 = kv_data["fp8"][0].view(torch.uint8).reshape(-1, 576).cpu().numpy() if "fp8" in kv_data else None
+    f8s = np.float32(kv_data["fp8"][1].item()) if "fp8" in kv_data else None
+    f4 = kv_data["mxfp4"][0].view(torch.uint8).reshape(-1, 288).cpu().numpy() if "mxfp4" in kv_data else None
+    f4s = kv_data["mxfp4"][1].view(torch.uint8).cpu().numpy() if "mxfp4" in kv_data else None
+    qbits = O.bf16_tensor_bits(q)
     threads = os.cpu_count() or 1
     torch.set_num_threads(threads)
-    t0 = time.perf_counter()
-    O.reference_path(qb, mode, caches, sub_ptr, local_idx, cfg["sm_scale"])
-    one = time.perf_counter() - t0
-    reps = max(1, min(20, int(budget_s / max(one, 1e-3))))
-    ts = []
-    for _ in range(reps):
+
+    def run(nb):
+        sub_ptr = indptr[: nb + 1]
+        rows = idx[: sub_ptr[-1]]
+        caches = {}
+        if f8 is not None:
+            caches.update(fp8_codes=f8[rows], fp8_scale=f8s)
+        if f4 is not None:
+            caches.update(fp4_packed=f4[rows], fp4_scales=f4s[rows])
         t0 = time.perf_counter()
-        O.reference_path(qb, mode, caches, sub_ptr, local_idx, cfg["sm_scale"])
-        ts.append(time.perf_counter() - t0)
+        O.reference_path(qbits[:nb], mode, caches, sub_ptr, np.arange(sub_ptr[-1]), cfg["sm_scale"])
+        return time.perf_counter() - t0, int(sub_ptr[-1])
+
+    # probe with the first sequence, then take as many leading sequences as
+    # one run of about budget/3 allows (all of them when it fits)
+    one, tok1 = run(1)
+    per_tok = one / max(tok1, 1)
+    nb = 1
+    while nb < B and per_tok * indptr[nb + 1] <= budget_s / 3:
+        nb += 1
+    ts = []
+    t_end = time.perf_counter() + budget_s
+    while len(ts) < 3 or (len(ts) < 10 and time.perf_counter() < t_end):
+        t, ntok = run(nb)
+        ts.append(t)
+        if time.perf_counter() > t_end and len(ts) >= 1:
+            break
     ts.sort()
     med = ts[len(ts) // 2]
-    scale = T / max(int(sub_ptr[-1]), 1)
+    scale = T / max(ntok, 1)
+    full = nb == B
+    sample = (f"whole config ({B} sequences, {T} tokens)" if full else
+              f"first {nb}/{B} sequences ({ntok}/{T} tokens), scaled by token share x{scale:.2f}")
     return {"value": round(med * scale * 1e6, 1), "unit": "us per call", "cores": threads, "kind": "port",
-            "sample": f"oracle reference path (quantize Q, dequantize KV, fp32 torch attention) on the first "
-                      f"{nb}/{B} sequences ({int(sub_ptr[-1])}/{T} tokens), median of {reps} reps, "
-                      f"scaled by token share x{scale:.2f}"}
+            "sample": f"oracle reference path (quantize Q, dequantize KV, fp32 torch attention): {sample}; "
+                      f"median of {len(ts)} reps", "full": full}
 
 
 def profile_decode(cids, reps):
@@ -317,7 +499,10 @@ def main(argv=None):
     ap.add_argument("--config", type=int, default=2, help="headline workload (BASELINE configs[1] = 2)")
     ap.add_argument("--only-headline", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-budget-s", type=float, default=10.0)
+    ap.add_argument("--cpu-budget-s", type=float, default=6.0, help="CPU-baseline time budget per config")
+    ap.add_argument("--no-probe", action="store_true", help="skip the per-config gather ceiling")
+    ap.add_argument("--gather-probe", action="store_true",
+                    help="sweep the gather-ceiling probe variants instead (own JSON line)")
     ap.add_argument("--append-tokens", type=int, default=0,
                     help="time the KV-cache append writer at this many tokens instead (own JSON line)")
     ap.add_argument("--neighbours", action="store_true",
@@ -340,27 +525,27 @@ def main(argv=None):
     if args.neighbours:
         print(json.dumps(bench_neighbours(args.steps, args.warmup)), flush=True)
         return 0
+    if args.gather_probe:
+        print(json.dumps(gather_probe_sweep(max(args.steps, 5))), flush=True)
+        return 0
     if args.profile_decode:
         profile_decode([args.config] if args.only_headline else sorted(inputs.CONFIGS), max(1, args.steps))
         return 0
     flush = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
     cids = [args.config] if args.only_headline else sorted(inputs.CONFIGS)
     per = {}
-    head_data = None
     for cid in cids:
-        res, data = time_config(cid, args.steps, args.warmup, flush)
+        res, data = time_config(cid, args.steps, args.warmup, flush, probe=not args.no_probe)
+        if not args.no_cpu:
+            log(f"[bench] config {cid}: cpu baseline")
+            res["cpu_baseline"] = cpu_baseline(cid, data, args.cpu_budget_s)
+            log(f"[bench] config {cid}: cpu {res['cpu_baseline']['value']} us ({res['cpu_baseline']['sample']})")
         per[str(cid)] = res
-        if cid == args.config:
-            head_data = data
-        else:
-            del data
+        del data
         torch.cuda.empty_cache()
     head = per[str(args.config)]
-    cpu = None
-    if not args.no_cpu:
-        log("[bench] cpu baseline")
-        cpu = cpu_baseline(args.config, head_data, args.cpu_budget_s)
     spec = inputs.CONFIGS[args.config]
+    traffic, traffic_src = measured_traffic(args.config)
     line = {
         "metric": METRIC,
         "value": head["us_per_call_mean"],
@@ -379,10 +564,11 @@ def main(argv=None):
                    "total_kv": head["total_kv"], "page_size": 1, "permuted_pages": spec["permute"],
                    "sm_scale": inputs.SM_SCALE},
         "roofline": {"bound": "hbm", "achieved": head["decode_hbm_GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": head["decode_hbm_frac"], "traffic": measured_traffic(args.config),
+                     "frac": head["decode_hbm_frac"], "traffic": traffic,
+                     "traffic_source_digest": traffic_src, "source_digest": source_digest(),
                      "kernel": "decode (mla decode_h16/decode_h128)",
                      "bytes_per_launch": head["bytes_alg_decode"], "avg_launch_us": head["us_decode_kernel_mean"]},
-        "cpu_baseline": cpu,
+        "cpu_baseline": head.get("cpu_baseline"),
         "per_config": per,
     }
     print(json.dumps(line), flush=True)

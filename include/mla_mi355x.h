@@ -208,6 +208,29 @@ int mla_decode_fwd_noalloc(const void* q_bf16, const void* k_cache, int64_t k_ro
 int64_t mla_noalloc_scratch_bytes(void);
 
 /*
+ * Diagnostic (no counterpart in the reference): the decode kernels' KV gather
+ * with no compute, to measure the HBM rate a cache layout and issue scheme
+ * can reach.  ntokens (a multiple of 64) entries of kv_indices are read in
+ * 64-token tiles spread evenly over `groups` work-groups of 64*waves threads.
+ *   layout 0: rows = fp8 cache (576 B read per token)
+ *   layout 1: rows = mxfp4 cache (288 B) + scales (18 B per token)
+ *   layout 2: layout 1 + v_rows = fp8 cache (512 B per token)
+ *   method 0: LDS-DMA ring, scales as 6 dword DMAs per tile (the scale buffer
+ *             needs 8 readable bytes past its last row's 18)
+ *   method 1: LDS-DMA ring, scales as 18 one-byte DMAs per tile
+ *   method 2: layout 0 by plain 16-byte loads into registers
+ *   method 3: contiguous stream of ntokens * row_stride bytes of rows (no
+ *             indices; waves = 4)
+ * Supported (layout, method, waves, stages): (0,0,4,2..4), (0,0,8,2|4),
+ * (1,0,4,3|4), (1,0,8,4), (1,1,4,3), (2,0,4|8,2), (2,1,4,2), (0,2,4|8,0),
+ * (any,3,4,any).  sink: 1 KiB of device memory.
+ */
+int mla_probe_gather(int layout, int method, int waves, int stages, int groups, const void* rows,
+                     int64_t row_stride, const void* scales, int64_t scale_stride, const void* v_rows,
+                     int64_t v_row_stride, const int32_t* kv_indices, int64_t ntokens, void* sink,
+                     void* stream);
+
+/*
  * Diagnostics (no counterpart in the reference): runs one wave of a built-in
  * check that pins an MFMA operand/accumulator layout or a conversion the
  * kernels rely on.  `in`/`out` are small device buffers whose layout per
