@@ -647,7 +647,7 @@ __device__ __forceinline__ void load_q128(const DecodeParams& p, int b, int head
 // registers), two tiles deep; the PV A operand (V^T) is read from the row-major
 // tile with ds_read_b64_tr_b8, so no transposed copy is ever written.  This
 // kernel serves the two-cache mode: fp4 K rows + e8m0 scales for QK, the fp8
-// cache's rows for V (the fp8-only mode runs decode_h128p_kernel below).
+// cache's rows for V (the fp8-only mode runs decode_h128f_kernel, decode_h128.hip).
 // Online softmax is rescaled lazily: the exponent base m only moves when a
 // head's tile max exceeds it by more than 8 (log2 units), so P <= 2^8 fits
 // e4m3 and O^T is touched by VALU only on those (rare) tiles.
@@ -966,391 +966,6 @@ __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams 
 }
 
 // ============================================================================
-// H = 128 with the fp8 cache (K = V = the 576-byte rows).  The work split is
-// decode_h128_kernel's: wave w owns heads 32w..+31, O^T lives in 256
-// accumulator registers, and the fixed-reference softmax carries each 32-token
-// half's offset on the e8m0 B scale of the PV MFMA.  What bounds this kernel is
-// the gather of the cache rows, so the ring is built for it: four 36 KiB
-// stages with rows issued three tiles ahead of their use and the slot indices
-// two tiles ahead of the rows.  Rows are stored unpadded with their 16-byte
-// chunks XOR-swizzled per row (the LDS-DMA fetches any global chunk into each
-// lane's fixed LDS position, so the swizzle costs nothing to write); it keeps
-// the K fragment reads (8 consecutive rows per 128 B) and the V^T transpose
-// reads (rows {0-3, 8-11} + const) on distinct banks.  MFMA issue is queued:
-// the PV MFMAs of tile t execute while the wave moves on to tile t+1, so P is
-// double-buffered (the softmax of t+1 must not overwrite registers those MFMAs
-// have yet to read), and the score accumulators are pinned to VGPRs by asm
-// (the builtin would put them in AGPRs, which O^T fills).
-// ============================================================================
-struct H128P {
-  static constexpr int RST = kQKDim;              // LDS row stride (576 B, chunks swizzled)
-  static constexpr int WIN = kTile * RST / 1024;  // 36 one-KiB DMA windows per tile
-  static constexpr int DPW = WIN / 4;             // 9 per wave
-  static constexpr int STAGE = WIN * 1024;
-  static constexpr int S = 4;                     // ring depth (tiles)
-  static constexpr int LEAD = S - 1;              // rows of tile t issued at tile t - LEAD
-  static constexpr int NSL = 8;                   // slot stages: slots of tile t issued at t - LEAD - 2
-  static constexpr int OFF_SLOT = S * STAGE;      // [NSL][64] int32 cache slots
-  static constexpr int OFF_VOTE = OFF_SLOT + NSL * 256;
-  static constexpr int LDS = OFF_VOTE + 16;
-};
-
-// XOR key of row r: rows 0..7 get 0..7; rows 8..15 the same keys with bit 2
-// flipped (the V^T reads of a 16-lane group pair row r with row r + 8)
-__device__ __forceinline__ int h128_key(int r) { return (r & 7) ^ ((r >> 1) & 4); }
-// LDS position of logical 16-B chunk c (0..35) of row r; an involution, so it
-// also maps a position back to its chunk.  Chunks 32..35 (the rope dims)
-// permute within their group of four.
-__device__ __forceinline__ int h128_chunk(int r, int c) {
-  const int x = h128_key(r);
-  return c < 32 ? (c ^ x) : (32 + ((c - 32) ^ (x & 3)));
-}
-
-// 32x32x64 fp8 MFMA with its accumulator in VGPRs.  The builtin gets AGPRs for
-// every MFMA of a kernel that uses AGPRs, and O^T already fills all 256 of them,
-// so the compiler would shuttle accumulators through VGPRs each tile; explicit
-// asm pins the score accumulators to VGPRs.  The compiler's hazard checks do
-// not see inside the asm, so each MFMA is fenced with s_nop (VALU writes of its
-// sources before, source reads after), and its result is read only after
-// mfma_drain: 32 wait states, above the 19 that a VALU read of a 16-pass XDL
-// result needs.
-__device__ __forceinline__ void mfma32_f8_vz(v16f& d, const v8i& a, const v8i& b) {
-  asm volatile("s_nop 1\n\tv_mfma_f32_32x32x64_f8f6f4 %0, %1, %2, 0\n\ts_nop 2" : "=&v"(d) : "v"(a), "v"(b));
-}
-__device__ __forceinline__ void mfma32_f8_vacc(v16f& d, const v8i& a, const v8i& b) {
-  asm volatile("s_nop 1\n\tv_mfma_f32_32x32x64_f8f6f4 %0, %1, %2, %0\n\ts_nop 2" : "+v"(d) : "v"(a), "v"(b));
-}
-__device__ __forceinline__ void mfma_drain(v16f& x, v16f& y) {
-  asm volatile("s_nop 15\n\ts_nop 15" : "+v"(x), "+v"(y));
-}
-
-template <bool IDX>
-__global__ __launch_bounds__(256, 1) void decode_h128p_kernel(const DecodeParams p) {
-  using C = H128P;
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[C::LDS];
-  const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
-
-  const int32_t* plan = p.plan;
-  if ((int)blockIdx.x >= plan[0]) return;
-  const int4 it = reinterpret_cast<const int4*>(plan + kPlanHeader)[blockIdx.x];
-  const int b = it.x, t_beg = it.y, t_end = it.z, slot = it.w;
-  const int ntok = t_end - t_beg;
-  const int ntiles = (ntok + kTile - 1) / kTile;
-
-  const int tid = threadIdx.x;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (feeds M0)
-  const int lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
-  const int head = 32 * w + l32;
-
-  // ---- Q^T B operand, K-step ks = dims 64ks .. +63 -------------------------------
-  v8i qv[9];
-  load_q128<32, 16>(p, b, head, hh, qv);
-  const float c = p.q_scale[0] * p.kv_scale[0] * p.sm_scale * kLog2e;
-  const float vscale = p.kv_scale[0];  // the 2^8 carried by P' is folded into the PV scale exponent
-
-  // ---- lane-constant LDS maps ----------------------------------------------------
-  // DMA: window u = w + 4k of a stage puts lane l at chunk position 64u + l =
-  // (row r, position j), which holds logical chunk h128_chunk(r, j); packed as
-  // (r << 10 | 16 chunk), two windows per register
-  uint32_t dmap[(C::DPW + 1) / 2];
-#pragma unroll
-  for (int k = 0; k < C::DPW; ++k) {
-    const int pidx = 64 * (w + 4 * k) + lane;
-    const int r = pidx / 36, j = pidx - 36 * r;
-    const uint32_t e = ((uint32_t)r << 10) | (uint32_t)(16 * h128_chunk(r, j));
-    if (k % 2 == 0) dmap[k / 2] = e;
-    else dmap[k / 2] |= e << 16;
-  }
-  // K fragment of K-step ks, token half u: row 32u + l32 (rows r and r + 32 share
-  // a key), logical chunks 4ks + 2hh + {0,1}, at byte 18432 u + 128 (ks >> 1) +
-  // kofs[ks & 1][j] for ks < 8 and 18432 u + kofs8[j] for ks = 8
-  int kofs[2][2], kofs8[2];
-  {
-    const int x = h128_key(l32);
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      kofs[0][j] = l32 * C::RST + 16 * ((2 * hh + j) ^ x);
-      kofs[1][j] = l32 * C::RST + 16 * ((4 + 2 * hh + j) ^ x);
-      kofs8[j] = l32 * C::RST + 16 * (32 + ((2 * hh + j) ^ (x & 3)));
-    }
-  }
-  // V^T fragment (PV A operand) of dim tile dt: four ds_read_b64_tr_b8; read cc of
-  // lane (G, m, oo) is row T0 + 16cc, T0 = 8(m >> 2) + 4hh + (m & 3) (all four rows
-  // share T0's key), logical chunk 2dt + (G & 1): byte 9216 cc + 128 (dt >> 2) +
-  // vofs[dt & 3]
-  int vofs[4];
-  {
-    const int G = lane >> 4, m = (lane & 15) >> 1, oo = lane & 1;
-    const int T0 = 8 * (m >> 2) + 4 * hh + (m & 3);
-    const int x = h128_key(T0);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) vofs[e] = T0 * C::RST + 16 * ((2 * e + (G & 1)) ^ x) + 8 * oo;
-  }
-
-  v16f o[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) o[i] = v16f{};
-  float m_ref = 0.f, l_run = 0.f;
-
-  // softmax state handed from tile t to the PV of tile t (run during tile t+1)
-  v8i pbh = v8i{}, pbl = v8i{};
-  int pscale = 127;
-
-  // ---- DMA issue -------------------------------------------------------------------
-  auto slot_of = [&](int t, int r, int pos0) -> int {
-    if constexpr (IDX) return reinterpret_cast<const int*>(smem + C::OFF_SLOT + (t % C::NSL) * 256)[r];
-    else return min(pos0 + r, t_end - 1);
-  };
-  // wave 0: the 64 slots of tile t (positions clamped into the item; tiles past
-  // the item fetch valid slots too, which keeps the vmcnt bookkeeping uniform)
-  auto issue_slots = [&](int t) {
-    if constexpr (IDX) {
-      if (w == 0) {
-        const int pos = min(t_beg + kTile * t + lane, t_end - 1);
-        dma4_to_lds(p.kv_indices + pos, lds0 + C::OFF_SLOT + (t % C::NSL) * 256);
-      }
-    }
-  };
-  auto issue_rows = [&](int t) {  // this wave's 9 windows of tile t
-    const int st = t % C::S;
-    const int pos0 = t_beg + kTile * t;
-    const uint32_t sbase = lds0 + st * C::STAGE;
-    int sl[C::DPW];
-    auto ent = [&](int k) -> uint32_t { return (dmap[k / 2] >> (16 * (k % 2))) & 0xFFFFu; };
-#pragma unroll
-    for (int k = 0; k < C::DPW; ++k) sl[k] = slot_of(t, (int)(ent(k) >> 10), pos0);  // reads before any DMA
-#pragma unroll
-    for (int k = 0; k < C::DPW; ++k)
-      dma16_to_lds(p.k_cache + ((uint64_t)(uint32_t)sl[k] * (uint32_t)p.k_row_stride + (ent(k) & 1023u)),
-                   sbase + 1024 * (w + 4 * k));
-  };
-  // Steady state: the pass of tile t issues slots(t + LEAD + 2) and rows(t + LEAD).
-  // The prologue issues what passes -3..-1 would have: slots(0..2) first (waited
-  // for), then rows(0), slots(3), rows(1), slots(4), rows(2).
-  auto prologue = [&]() {
-    pbh = v8i{};
-    pbl = v8i{};
-    pscale = 127;
-    issue_slots(0);
-    issue_slots(1);
-    issue_slots(2);
-    wait_vmcnt<0>();
-    lds_barrier();
-    issue_rows(0);
-    issue_slots(3);
-    if (ntiles > 1) issue_rows(1);
-    issue_slots(4);
-    if (ntiles > 2) issue_rows(2);
-  };
-  // At the top of tile t, rows(t) and slots(t + LEAD) must have landed.  Issued
-  // after rows(t), in order: slots(t+3), rows(t+1), slots(t+4), rows(t+2) (rows
-  // only for tiles of the item; wave 0 alone issues slots).
-  auto wait_tile = [&](int t) {
-    const bool s0 = IDX && w == 0;
-    if (t + 2 < ntiles) {
-      if (s0) wait_vmcnt<2 * C::DPW + 1>();
-      else wait_vmcnt<2 * C::DPW>();
-    } else if (t + 1 < ntiles) {
-      if (s0) wait_vmcnt<C::DPW + 2>();
-      else wait_vmcnt<C::DPW>();
-    } else {
-      if (s0) wait_vmcnt<2>();
-      else wait_vmcnt<0>();
-    }
-  };
-
-  // ---- per-tile pieces ----------------------------------------------------------------
-  auto qk = [&](int st, v16f& s0, v16f& s1) {
-    const uint8_t* kt = smem + st * C::STAGE;
-    auto kfrag = [&](int ks, int u) -> v8i {
-      const uint8_t* a = kt + 18432 * u + (ks < 8 ? kofs[ks & 1][0] + 128 * (ks >> 1) : kofs8[0]);
-      const uint8_t* bb = kt + 18432 * u + (ks < 8 ? kofs[ks & 1][1] + 128 * (ks >> 1) : kofs8[1]);
-      const uint4 lo = *reinterpret_cast<const uint4*>(a);
-      const uint4 hi = *reinterpret_cast<const uint4*>(bb);
-      return v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-    };
-    v8i a0n = kfrag(0, 0), a1n = kfrag(0, 1);
-#pragma unroll
-    for (int ks = 0; ks < 9; ++ks) {
-      const v8i a0 = a0n, a1 = a1n;
-      if (ks < 8) {
-        a0n = kfrag(ks + 1, 0);
-        a1n = kfrag(ks + 1, 1);
-      }
-      if (ks == 0) {
-        mfma32_f8_vz(s0, a0, qv[0]);
-        mfma32_f8_vz(s1, a1, qv[0]);
-      } else {
-        mfma32_f8_vacc(s0, a0, qv[ks]);
-        mfma32_f8_vacc(s1, a1, qv[ks]);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    mfma_drain(s0, s1);
-  };
-  auto vfrag = [&](uint32_t vbase, int dt) -> v8i {
-    const uint32_t vb = vbase + 128 * (dt >> 2) + vofs[dt & 3];
-    const v2i r0 = lds_read_tr8(vb);
-    const v2i r1 = lds_read_tr8(vb + 16 * C::RST);
-    const v2i r2 = lds_read_tr8(vb + 32 * C::RST);
-    const v2i r3 = lds_read_tr8(vb + 48 * C::RST);
-    return v8i{r0[0], r0[1], r1[0], r1[1], r2[0], r2[1], r3[0], r3[1]};
-  };
-
-  // O^T accumulates sum_n V_n 2^(s_n - m_ref) against a fixed per-lane (head)
-  // reference, the first tile's ceil(max).  A tile whose max lies more than
-  // kRebase above m_ref makes the whole block restart the item with m_ref =
-  // the running max (block-wide vote through LDS, read one tile later, before
-  // that tile's PV runs).
-  uint8_t* vote = smem + C::OFF_VOTE;  // [2][4] wave flags, double-buffered by tile parity
-  float m_seen = neg_inf();
-  bool have_ref = false;
-
-  // P (and its scale) is double-buffered by pass parity: the PV MFMAs of tile t
-  // are still queued while the softmax of tile t+1 writes the other buffer.
-  v8i pbh2 = v8i{}, pbl2 = v8i{};
-  int pscale2 = 127;
-  // one tile; returns true when the block votes to restart the item
-  auto pass = [&](int ti, v8i& ph, v8i& pl, int& psc) -> bool {
-    const int st = ti % C::S;
-    const int nval = ntok - kTile * ti;
-    wait_tile(ti);
-    lds_barrier();  // tile ti visible; every wave is done with tile ti-1's stage
-    if (ti > 0 &&
-        __builtin_amdgcn_readfirstlane(*reinterpret_cast<const uint32_t*>(vote + 4 * ((ti - 1) & 1))) != 0)
-      return true;
-    issue_slots(ti + C::LEAD + 2);
-    if (ti + C::LEAD < ntiles) issue_rows(ti + C::LEAD);
-
-    v16f s0, s1;
-    qk(st, s0, s1);
-    // s_u[r] = raw score(token 32u + 8(r/4) + 4hh + r%4, head); masked past the item
-    if (nval < kTile) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int tk = 8 * (r >> 2) + 4 * hh + (r & 3);
-        if (tk >= nval) s0[r] = neg_inf();
-        if (32 + tk >= nval) s1[r] = neg_inf();
-      }
-    }
-    // per-half maxima, offsets, vote
-    float mx0 = neg_inf(), mx1 = neg_inf();
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      mx0 = fmaxf(mx0, s0[r]);
-      mx1 = fmaxf(mx1, s1[r]);
-    }
-    mx0 = fmaxf(mx0, shfl_xor_f(mx0, 32));
-    mx1 = fmaxf(mx1, shfl_xor_f(mx1, 32));
-    const float m0 = __builtin_ceilf(mx0 * c), m1 = __builtin_ceilf(mx1 * c);  // -inf: empty half
-    const float mt = fmaxf(m0, m1);
-    if (!have_ref) m_ref = mt;  // first tile of the first pass
-    have_ref = true;
-    m_seen = fmaxf(m_seen, mt);
-    const bool over = __any(mt > m_ref + kRebase);
-    if (lane == 0) vote[4 * (ti & 1) + w] = over ? 1 : 0;
-    const float e0 = m0 == neg_inf() ? m_ref : m0, e1 = m1 == neg_inf() ? m_ref : m1;
-    const float d0 = fminf(fmaxf(e0 - m_ref, -160.f), 160.f), d1 = fminf(fmaxf(e1 - m_ref, -160.f), 160.f);
-    psc = min(max((int)(hh ? d1 : d0) - 8 + 127, 0), 254);
-    // P'_u = 2^(c s - m_u + 8), the row sums, and the P'^T B operand: byte
-    // 16u + 4q + i <-> token 32u + 8q + 4hh + i, hi + lo fp8 terms
-    float ps0 = 0.f, ps1 = 0.f;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      s0[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[r], c, 8.f - e0));
-      s1[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[r], c, 8.f - e1));
-      ps0 += s0[r];
-      ps1 += s1[r];
-    }
-    l_run += ps0 * __builtin_amdgcn_exp2f(d0 - 8.f) + ps1 * __builtin_amdgcn_exp2f(d1 - 8.f);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      uint32_t h0, l0, h1, l1;
-      pack4_fp8_split(s0[4 * q], s0[4 * q + 1], s0[4 * q + 2], s0[4 * q + 3], h0, l0);
-      pack4_fp8_split(s1[4 * q], s1[4 * q + 1], s1[4 * q + 2], s1[4 * q + 3], h1, l1);
-      ph[q] = (int)h0;
-      pl[q] = (int)l0;
-      ph[4 + q] = (int)h1;
-      pl[4 + q] = (int)l1;
-    }
-    // O^T += V^T . P^T: dim tiles in pairs (hi and lo MFMAs of one accumulator
-    // not back to back), V^T fragments one pair ahead
-    const uint32_t vst = lds0 + st * C::STAGE;
-    v8i an0 = vfrag(vst, 0), an1 = vfrag(vst, 1);
-#pragma unroll
-    for (int dt = 0; dt < 16; dt += 2) {
-      const v8i a0 = an0, a1 = an1;
-      if (dt < 14) {
-        an0 = vfrag(vst, dt + 2);
-        an1 = vfrag(vst, dt + 3);
-      }
-      o[dt] = mfma32_f8_bscale(a0, ph, psc, o[dt]);
-      o[dt + 1] = mfma32_f8_bscale(a1, ph, psc, o[dt + 1]);
-      o[dt] = mfma32_f8_bscale(a0, pl, psc, o[dt]);
-      o[dt + 1] = mfma32_f8_bscale(a1, pl, psc, o[dt + 1]);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    return false;
-  };
-
-  for (;;) {
-    if (ntiles > 0) prologue();
-    bool restart = false;
-    for (int ti = 0; ti < ntiles && !restart; ti += 2) {
-      restart = pass(ti, pbh, pbl, pscale);
-      if (!restart && ti + 1 < ntiles) restart = pass(ti + 1, pbh2, pbl2, pscale2);
-    }
-    if (!restart && ntiles > 0) {
-      lds_barrier();  // the last tile's votes
-      restart = __builtin_amdgcn_readfirstlane(
-                    *reinterpret_cast<const uint32_t*>(vote + 4 * ((ntiles - 1) & 1))) != 0;
-    }
-    if (!restart) break;
-    // drain the ring (the prologue reuses it), then start over from m_ref = running max
-    wait_vmcnt<0>();
-    lds_barrier();
-    m_ref = m_seen;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) o[i] = v16f{};
-    l_run = 0.f;
-  }
-
-  // ---- finish ---------------------------------------------------------------------
-  const float L = l_run + shfl_xor_f(l_run, 32);
-  const float inv = L > 0.f ? vscale / L : 0.f;
-  if (slot < 0) {
-    if (p.lse_out != nullptr && hh == 0)
-      p.lse_out[(int64_t)b * 128 + head] = L > 0.f ? (m_ref + __log2f(L)) * kLn2 : neg_inf();
-    uint16_t* orow = p.out + ((int64_t)b * 128 + head) * kVDim;
-#pragma unroll
-    for (int dt = 0; dt < 16; ++dt) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int d = 32 * dt + 8 * q + 4 * hh;
-        const uint32_t lo = f32_to_bf16_bits(o[dt][4 * q] * inv) | (f32_to_bf16_bits(o[dt][4 * q + 1] * inv) << 16);
-        const uint32_t hi = f32_to_bf16_bits(o[dt][4 * q + 2] * inv) | (f32_to_bf16_bits(o[dt][4 * q + 3] * inv) << 16);
-        *reinterpret_cast<uint2*>(orow + d) = make_uint2(lo, hi);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  } else {
-    uint16_t* prow = p.part_o + ((int64_t)slot * 128 + head) * kVDim;
-#pragma unroll
-    for (int dt = 0; dt < 16; ++dt) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int d = 32 * dt + 8 * q + 4 * hh;
-        const uint32_t lo = f32_to_bf16_bits(o[dt][4 * q] * inv) | (f32_to_bf16_bits(o[dt][4 * q + 1] * inv) << 16);
-        const uint32_t hi = f32_to_bf16_bits(o[dt][4 * q + 2] * inv) | (f32_to_bf16_bits(o[dt][4 * q + 3] * inv) << 16);
-        *reinterpret_cast<uint2*>(prow + d) = make_uint2(lo, hi);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    if (hh == 0) p.part_lse[(int64_t)slot * 128 + head] = L > 0.f ? m_ref + __log2f(L) : neg_inf();
-  }
-}
-
-// ============================================================================
 // LSE combine: out[b,h,:] = sum_s 2^(lse_s - M) O_s / sum_s 2^(lse_s - M)
 // grid (batch, H/16, 4): block = 16 heads x 128 dims, thread = (head, 8 dims);
 // the split partials are read in batches of 8 so their loads overlap
@@ -1423,7 +1038,7 @@ static hipError_t launch_decode_t(const DecodeParams& p, int kv_mode, int grid, 
   } else if (p.num_heads == 128) {
     if (QB) return hipErrorInvalidValue;  // the H = 128 kernel takes a quantized Q
     switch (kv_mode) {
-      case 0: hipLaunchKernelGGL((decode_h128p_kernel<IDX>), dim3(grid), dim3(256), 0, stream, p); break;
+      case 0: return launch_decode_h128f(p, grid, stream);
       case 2: hipLaunchKernelGGL((decode_h128_kernel<IDX>), dim3(grid), dim3(256), 0, stream, p); break;
       default: return hipErrorInvalidValue;
     }

@@ -1,0 +1,699 @@
+// MLA absorbed decode, 128 heads with the fp8 cache (K = V = the 576-byte
+// rows), for gfx950.
+//
+// Work split: one work-group of 4 waves per CU runs one work item {batch,
+// token range, slot} of the on-device plan.  Wave w owns heads 32w .. 32w+31
+// for every token of the item and all 512 latent dims: Q^T (the QK B operand,
+// 72 VGPRs) stays in registers, O^T (the PV accumulator, 256 AGPRs) never
+// leaves them, and the softmax needs no cross-wave exchange.  This split reads
+// each K and V byte from LDS once per 32 heads, the fewest LDS reads of any
+// split that keeps Q in registers.
+//
+// Tiles are 32 tokens, pairs of tiles 64.  Per tile a wave runs 9 QK MFMAs
+// (32x32x64, S^T = K . Q^T); per pair 32 PV MFMAs (O^T += V^T . P'^T, K = the
+// pair's 64 tokens): P' split into two fp8 terms, hi = e4m3(x) and lo =
+// e4m3(x - hi), each its own MFMA against the same V^T fragment (16 dim tiles
+// x 2 terms).  Each lane's own QK outputs are exactly the 16 tokens its P'^T
+// bytes of that tile need, so P never crosses lanes.  The loop is a software
+// pipeline: iteration t runs QK(t), softmax(t - 1) and half of the PV of the
+// pair whose softmax ended before it (pair q - 2's second half in the even
+// iteration of pair q, pair q - 1's first half in the odd one).
+//
+// A wave issues one MFMA per 64 cycles and only about a dozen other
+// instructions fit beside each (one wave per SIMD), so the iteration is a
+// static schedule of 25 MFMA slots (QK steps at slots 0, 3, .., 24, PV in
+// between) with the other work spread one slice per slot: fragment loads four
+// to six slots ahead of their MFMA, one of 22 softmax steps, one row DMA every
+// two or three slots of the pair.  Addresses move once per tile, in place.
+//
+// LDS: a 4-stage ring of 64-row pairs (608-byte rows: 576 + 32 of padding,
+// 16-byte chunks of row r XOR-swizzled by (r >> 2) & 7, which keeps both the K
+// fragment reads (ds_read_b128) and the V^T transpose reads
+// (ds_read_b64_tr_b8) near their bank-conflict floor).  Rows arrive by LDS-DMA
+// (global_load_lds_dwordx4) two pairs ahead of use; a pair's 64 slot indices
+// arrive by one dword LDS-DMA four pairs ahead of its rows.  Two work-group
+// barriers per pair: one once every wave has read the last V^T of pair q - 2
+// (its stage then takes pair q + 2's rows), one once pair q + 1 has landed.
+// The LDS-DMA writes lane l of a 1 KiB window to position 64u + l of the
+// pair's stage, so each lane fetches whichever chunk its position holds
+// (padding positions re-fetch chunk 0 of their row, a cache hit).  Q comes the
+// same way, into stages 2-3 before the first rows(2) land there.
+//
+// Softmax: per head a reference m_ref (the first tile's ceil max); a tile's
+// P' = 2^(c s - m_t + 8) with m_t its ceil max, and the PV MFMA's e8m0 B scale
+// carries 2^(m_t - m_ref - 8), so O^T accumulates sum V 2^(s - m_ref) with no
+// rescale.  A tile max more than 96 above m_ref (the accumulators could
+// overflow) is clamped and flagged; at the end of the item a flag from any
+// wave makes the work-group run the item again with every head's m_ref set to
+// its running max over the whole item, which no tile then exceeds.
+//
+// Behavioural reference: mixed-mla/asm_dumps/aiter_mla.py:149-470 (interface,
+// 128-head folding :318-353), TASK/reference.py:349-369 (numerics).
+#include <type_traits>
+
+#include "mla_internal.hpp"
+
+namespace mla {
+namespace {
+
+constexpr float kLog2eF = 1.4426950408889634f;
+constexpr float kLn2F = 0.6931471805599453f;
+constexpr float kRebaseF = 96.0f;
+
+struct G128 {
+  static constexpr int RST = 608;               // LDS row stride
+  static constexpr int CPR = RST / 16;          // 38 chunk positions per row (36 used)
+  static constexpr int HT = 32;                 // tokens per tile
+  static constexpr int TSTAGE = HT * RST;       // 19456 B per tile
+  static constexpr int PSTAGE = 2 * TSTAGE;     // a pair of tiles: 38 one-KiB DMA windows
+  static constexpr int WIN = PSTAGE / 1024;
+  static constexpr int NP = 4;                  // pair stages: pairs q-1 (V), q (K), q+1, q+2 (in flight)
+  static constexpr int NSL = 8;                 // slot stages (one per pair)
+  static constexpr int DMAX = (WIN + 3) / 4;    // windows of waves 0, 1 (waves 2, 3: DMAX - 1)
+  static constexpr int OFF_SLOT = NP * PSTAGE;
+  static constexpr int OFF_FLAG = OFF_SLOT + NSL * 256;  // [4] per-wave overflow flags
+  static constexpr int LDS = OFF_FLAG + 16;
+  static_assert(WIN == 38 && DMAX == 10, "DMA window split");
+  static_assert(LDS <= 160 * 1024, "LDS");
+};
+
+__device__ __forceinline__ int g128_key(int r) { return (r >> 2) & 7; }
+// LDS chunk position (0..35) of logical chunk c of row r; an involution
+__device__ __forceinline__ int g128_pos(int r, int c) {
+  const int x = g128_key(r);
+  return c < 32 ? (c ^ x) : 32 + ((c - 32) ^ (x & 3));
+}
+
+__device__ __forceinline__ float ninf() { return -__builtin_inff(); }
+
+// QK: 32x32x64 fp8 MFMA with its accumulator in VGPRs (O^T holds all AGPRs, and
+// the builtin would give every MFMA of the kernel an AGPR accumulator).  All
+// MFMAs are issued by asm so that each keeps its place in the source order
+// (the builtins are pure values the compiler may move past the MFMAs they are
+// meant to interleave with).  The compiler does not see these MFMAs, so each is
+// fenced with s_nop (VALU writes of its sources before, source reads after),
+// and a result is read by VALU only after a drain (32 wait states; a VALU read
+// of a 16-pass XDL result needs 19).  A dependent chain on one accumulator
+// needs no wait states.
+__device__ __forceinline__ void qk_first(v16f& d, const v8i& a, const v8i& b) {
+  asm volatile("s_nop 1\n\tv_mfma_f32_32x32x64_f8f6f4 %0, %1, %2, 0\n\ts_nop 2" : "=&v"(d) : "v"(a), "v"(b));
+}
+__device__ __forceinline__ void qk_acc(v16f& d, const v8i& a, const v8i& b) {
+  asm volatile("s_nop 1\n\tv_mfma_f32_32x32x64_f8f6f4 %0, %1, %2, %0\n\ts_nop 2" : "+v"(d) : "v"(a), "v"(b));
+}
+__device__ __forceinline__ void drain_v(v16f& x) { asm volatile("s_nop 15\n\ts_nop 15" : "+v"(x)); }
+// PV: O^T += V^T . P'^T with an e8m0 scale on B (one per lane: its head), A at
+// unit scale; accumulator in AGPRs
+__device__ __forceinline__ void pv_mfma(v16f& acc, const v8i& a, const v8i& b, int bscale) {
+  asm volatile("s_nop 1\n\tv_mfma_scale_f32_32x32x64_f8f6f4 %0, %1, %2, %0, %3, %4 op_sel_hi:[0,0,0]"
+               : "+a"(acc)
+               : "v"(a), "v"(b), "v"(127), "v"(bscale));
+}
+// v_permlane32_swap of x with itself: each lane ends with its own value and
+// its partner's (lane +- 32)
+__device__ __forceinline__ float xhalf_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xhalf_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+// max of three scores (no NaN canonicalization: the scores are MFMA outputs)
+__device__ __forceinline__ float max3f(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+// x = -inf where pos >= lim (one compare into VCC and one select, so masking
+// a tile holds no per-element lane masks)
+__device__ __forceinline__ float mask_ge(float x, int pos, int lim) {
+  asm("v_cmp_le_i32 vcc, %2, %1\n\tv_cndmask_b32 %0, %0, %3, vcc"
+      : "+v"(x)
+      : "v"(pos), "v"(lim), "v"(ninf())
+      : "vcc");
+  return x;
+}
+// {hi, lo}: hi = e4m3(x), lo = e4m3(x - hi) of four values in [0, 448)
+__device__ __forceinline__ int2 split4(float a, float b, float c, float d) {
+  const uint32_t h = pack4_fp8(a, b, c, d);
+  const v2f h01 = __builtin_amdgcn_cvt_pk_f32_fp8((int)h, false);
+  const v2f h23 = __builtin_amdgcn_cvt_pk_f32_fp8((int)h, true);
+  return make_int2((int)h, (int)pack4_fp8(a - h01[0], b - h01[1], c - h23[0], d - h23[1]));
+}
+
+template <int I>
+using Ic = std::integral_constant<int, I>;
+
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(Ic<B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
+// The static schedule of one pair of iterations: 50 MFMA slots, slot i of an
+// iteration (0..24) issues QK step i / 3 when i % 3 == 0, else PV dim tile
+// 2 (i / 3) + i % 3 - 1.  A wave issues one MFMA per 64 cycles and about a
+// dozen other instructions fit beside each one, so the other work is spread
+// one slice per slot: fragment loads a few slots ahead of their MFMA, one
+// softmax step, one DMA every fourth slot of the pair.
+struct H128Sched {
+  static constexpr int kSlots = 25;
+  static constexpr bool is_qk(int i) { return i % 3 == 0; }
+  // PV slot i: group g = i / 3 (dim tile 8h + g of the iteration's half h of
+  // the pair's PV), term i % 3 - 1 (0: hi, 1: lo), both terms on one V^T fragment
+  // K fragment loaded at slot i: step g = 2..8 of this tile six slots ahead of
+  // QK g, steps 0 and 1 of the next tile (returned as 9, 10) at slots 20, 22
+  static constexpr int kload(int i) {
+    if (i <= 18 && i % 3 == 0) return i / 3 + 2;
+    if (i == 20) return 9;
+    if (i == 22) return 10;
+    return -1;
+  }
+  // V^T fragment of group g loaded at slot 3g - 3 (g = 1..7), group 0 of the
+  // next iteration (returned as 8) at slot 22
+  static constexpr int vload(int i) {
+    if (i <= 18 && i % 3 == 0) return i / 3 + 1;
+    if (i == 22) return 8;
+    return -1;
+  }
+  // K addresses move to the next tile after the last K load of the tile; V^T
+  // addresses to the next pair in iteration 0, after its last V^T load
+  static constexpr int kRebaseK = 19, kRebaseV = 21;
+  // softmax step k of the previous tile at iteration slot k + 2
+  static constexpr int kSoftSteps = 22;
+  // pair slots: the slot-index DMA; the barrier after the last V^T read of
+  // pair q - 2 (its stage then takes the rows of pair q + 2); row DMA k at
+  // dma_slot(k), its slot index read two slots before; the built P' becomes
+  // the PV operand at the start of iteration 1; the barrier that publishes
+  // pair q + 1 (iteration 1, slot 20, before that slot's K load: the first
+  // read of the next pair)
+  static constexpr int kSlotDma = 1;
+  static constexpr int kStageFree = 20;
+  static constexpr int dma_slot(int k) { return 21 + 5 * (k / 2) + 2 * (k % 2); }
+  static constexpr int row_dma(int s) {
+    for (int k = 0; k < 10; ++k)
+      if (dma_slot(k) == s) return k;
+    return -1;
+  }
+  static constexpr int row_read(int s) {
+    for (int k = 0; k < 10; ++k)
+      if (dma_slot(k) - 2 == s) return k;
+    return -1;
+  }
+  static constexpr int kCopy = 25;
+  static constexpr int kBarrier = 45;
+};
+
+template <bool IDX>
+__global__ __launch_bounds__(256, 1) void decode_h128f_kernel(const DecodeParams p) {
+  using C = G128;
+  using SC = H128Sched;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[C::LDS];
+  const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
+
+  // the item count and this item are read together (no dependent round trip;
+  // the plan has room for max_items >= gridDim.x items)
+  const int32_t* plan = p.plan;
+  const int nitems = plan[0];
+  const int4 it = reinterpret_cast<const int4*>(plan + kPlanHeader)[blockIdx.x];
+  if ((int)blockIdx.x >= nitems) return;
+  const int b = it.x, t_beg = it.y, t_end = it.z, slot = it.w;
+  const int ntok = t_end - t_beg;
+  const int n = (ntok + C::HT - 1) / C::HT;  // 32-token tiles
+  const int npair = (n + 1) / 2;             // pairs of tiles (the DMA and barrier unit)
+
+  const int tid = threadIdx.x;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (feeds M0)
+  const int lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
+  const int head = 32 * w + l32;
+
+  // ---- slot indices of pairs 0, 1 first: their round trip overlaps the Q load -
+  // wave 0: the 64 slot indices of pair q (positions clamped into the item:
+  // pairs past its end fetch valid slots too, so every pair issues the same
+  // DMAs and the vmcnt counts are uniform)
+  auto issue_slots = [&](int q) __attribute__((always_inline)) {
+    if constexpr (IDX) {
+      asm volatile("" : "+s"(q));  // the address is formed at the call, not kept live from the entry
+      if (w == 0) {
+        const int pos = min(t_beg + 64 * q + lane, t_end - 1);
+        dma4_to_lds(p.kv_indices + pos, lds0 + C::OFF_SLOT + (q % C::NSL) * 256);
+      }
+    }
+  };
+  // ---- Q: wave w's 32 head rows (18 KiB, contiguous in memory) go by LDS-DMA
+  // into pair stages 2-3, which the first rows(2) DMA overwrites only after the
+  // barrier that follows the Q^T register reads; Q then needs no compiler-
+  // tracked global load (whose conservative wait would also drain the row DMAs)
+  constexpr int kQWin = 32 * kQKDim / 1024;  // 18 one-KiB windows per wave
+  const uint32_t q_lds = lds0 + 2 * C::PSTAGE + w * 32 * kQKDim;
+  auto issue_q = [&]() __attribute__((always_inline)) {
+    const uint8_t* qsrc = p.q_fp8 + ((int64_t)b * 128 + 32 * w) * kQKDim + 16 * lane;
+    asm volatile("" : "+v"(qsrc));  // the window addresses are formed here, not kept live from the entry
+#pragma unroll
+    for (int k = 0; k < kQWin; ++k) dma16_to_lds(qsrc + 1024 * k, q_lds + 1024 * k);
+  };
+  // Q^T B operand: K-step ks = dims 64ks .. +63 (lane half hh: 32hh .. +31)
+  v8i qv[9];
+  auto read_q = [&]() __attribute__((always_inline)) {
+    typedef __attribute__((address_space(3))) v4i lds_v4i_q;
+    const uint32_t a = q_lds + l32 * kQKDim + 32 * hh;
+#pragma unroll
+    for (int ks = 0; ks < 9; ++ks) {
+      const v4i lo = *(const lds_v4i_q*)(uintptr_t)(a + 64 * ks);
+      const v4i hi = *(const lds_v4i_q*)(uintptr_t)(a + 64 * ks + 16);
+      qv[ks] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    }
+  };
+  const float c = p.q_scale[0] * p.kv_scale[0] * p.sm_scale * kLog2eF;
+  const float vscale = p.kv_scale[0];
+
+  // ---- DMA maps ---------------------------------------------------------------
+  // window u = w + 4k of a pair stage puts lane l at chunk position 64u + l =
+  // (row r of the pair, position j); it fetches logical chunk g128_pos(r, j)
+  // (chunk 0 for the two padding positions); packed (r << 10 | byte offset),
+  // two windows per register
+  uint32_t dmap[C::DMAX / 2];
+#pragma unroll
+  for (int k = 0; k < C::DMAX; ++k) {
+    const int pidx = min(64 * (w + 4 * k) + lane, 64 * C::WIN - 1);
+    const int r = pidx / C::CPR, j = pidx - C::CPR * r;
+    const uint32_t e = ((uint32_t)r << 10) | (uint32_t)(16 * (j < 36 ? g128_pos(r, j) : 0));
+    if (k % 2 == 0) dmap[k / 2] = e;
+    else dmap[k / 2] |= e << 16;
+  }
+  // Window k of pair rq: its slot (read from the pair's slot-ring stage at
+  // sbase) and its DMA into the pair's stage (stage_w: the stage plus 1 KiB w;
+  // window k lands 4 KiB k further).  k is a compile-time constant at every
+  // call: the map register and its half are fixed.
+  auto row_slot = [&](int k, int rq, uint32_t sbase) __attribute__((always_inline)) -> int {
+    uint32_t d = dmap[k / 2];
+    asm volatile("" : "+v"(d));  // opaque map: its decode is not hoisted out of the loop
+    const uint32_t e = (d >> (16 * (k % 2))) & 0xFFFFu;
+    if constexpr (IDX) {
+      typedef __attribute__((address_space(3))) int lds_int;
+      return *(const lds_int*)(uintptr_t)(sbase + ((e >> 8) & 0xFCu));  // 4r: entry r of the ring stage
+    } else {
+      return min(t_beg + 64 * rq + (int)(e >> 10), t_end - 1);
+    }
+  };
+  auto row_dma = [&](int k, int sl, uint32_t stage_w) __attribute__((always_inline)) {
+    if (k < C::DMAX - 1 || w < 2) {
+      uint32_t d = dmap[k / 2];
+      asm volatile("" : "+v"(d));
+      const uint32_t off = (d >> (16 * (k % 2))) & 1023u;
+      const uint8_t* src = p.k_cache + ((uint64_t)(uint32_t)sl * (uint32_t)p.k_row_stride + off);
+      asm volatile("s_add_u32 m0, %0, %1\n\tglobal_load_lds_dwordx4 %2, off"
+                   :
+                   : "s"(stage_w), "i"(4096 * k), "v"(src)
+                   : "memory", "m0");
+    }
+  };
+  auto stage_of = [&](int q) __attribute__((always_inline)) -> uint32_t {  // pair q's stage + 1 KiB w
+    return __builtin_amdgcn_readfirstlane(lds0 + (q % C::NP) * C::PSTAGE + 1024 * w);
+  };
+  auto sring_of = [&](int q) __attribute__((always_inline)) -> uint32_t {  // pair q's slot-ring stage
+    return __builtin_amdgcn_readfirstlane(lds0 + C::OFF_SLOT + (q % C::NSL) * 256);
+  };
+  auto issue_rows = [&](int q) __attribute__((always_inline)) {
+    const uint32_t stw = stage_of(q), sb = sring_of(q);
+    int sl[C::DMAX];
+#pragma unroll
+    for (int k = 0; k < C::DMAX; ++k) sl[k] = row_slot(k, q, sb);  // every read before the first DMA
+#pragma unroll
+    for (int k = 0; k < C::DMAX; ++k) row_dma(k, sl[k], stw);
+  };
+  // rows(q) have landed once the DMAs issued after them are all that is
+  // outstanding: the next pair's slot indices (wave 0) and its rows (ten
+  // windows for waves 0 and 1, nine for waves 2 and 3)
+  auto wait_rows = [&]() __attribute__((always_inline)) {
+    if (w == 0) wait_vmcnt<IDX ? C::DMAX + 1 : C::DMAX>();
+    else if (w == 1) wait_vmcnt<C::DMAX>();
+    else wait_vmcnt<C::DMAX - 1>();
+  };
+  // the same near the end of the item, where no rows follow (only the slot
+  // indices of wave 0)
+  auto wait_rows_last = [&]() __attribute__((always_inline)) {
+    if (IDX && w == 0) wait_vmcnt<1>();
+    else wait_vmcnt<0>();
+  };
+
+  // ---- lane-constant fragment offsets -----------------------------------------
+  // K fragment (QK A operand) of K-step ks: row l32 of the tile, logical chunks
+  // 4ks + 2hh + {0, 1} (ks < 8) or 32 + 2hh + {0, 1} (ks = 8).  Rows r and r + 32
+  // share a key, so the offsets hold for both tiles of a pair.
+  // ka[2 (ks & 1) + j] + 128 (ks >> 1) (ks < 8), ka[4 + j] (ks = 8): LDS
+  // addresses of the current K tile, moved along the ring in place.
+  uint32_t ka[6];
+  // (the init lambdas derive everything from an opaque copy of the lane id, so
+  // the addresses are formed where they are needed, not kept live from the entry)
+  auto init_ka = [&]() __attribute__((always_inline)) {
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    const int r = ln & 31, h2 = (ln >> 5) * 2, x = g128_key(r);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      ka[j] = lds0 + r * C::RST + 16 * ((h2 + j) ^ x);
+      ka[2 + j] = lds0 + r * C::RST + 16 * ((4 + h2 + j) ^ x);
+      ka[4 + j] = lds0 + r * C::RST + 16 * (32 + ((h2 + j) ^ (x & 3)));
+    }
+  };
+  // V^T fragment (PV A operand) of dim tile dt (dims 32dt .. +31) over the 64
+  // tokens of a pair: four ds_read_b64_tr_b8, read cc of lane (G, m, oo) is
+  // row T0 + 16cc of the pair's first tile (bytes 8cc .. +7) and of its second
+  // tile (bytes 16 + 8cc .. +7), T0 = 8(m >> 2) + 4hh + (m & 3), logical chunk
+  // 2dt + (G & 1), byte 8oo: byte 16u + 4q + i <-> token 8q + 4hh + i of tile
+  // u, the order of the lane's own scores.  Row T0 + 16cc has key x0 ^ 4cc,
+  // x0 = T0 >> 2.  va[4cc + (dt & 3)] + 128 (dt >> 2) (+ TSTAGE): LDS
+  // addresses of the PV pair's first (second) tile.
+  uint32_t va[8];
+  auto init_va = [&]() __attribute__((always_inline)) {
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    const int G = ln >> 4, m = (ln & 15) >> 1, oo = ln & 1;
+    const int T0 = 8 * (m >> 2) + 4 * (ln >> 5) + (m & 3);
+    const int x0 = T0 >> 2;
+#pragma unroll
+    for (int cc = 0; cc < 2; ++cc)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)  // pair -2: stage 2 (never read by an MFMA)
+        va[4 * cc + e] = lds0 + 2 * C::PSTAGE + (T0 + 16 * cc) * C::RST +
+                         16 * ((2 * e + (G & 1)) ^ (x0 ^ (4 * cc))) + 8 * oo;
+  };
+  typedef __attribute__((address_space(3))) v4i lds_v4i;
+  v8i kf[3];
+  v8i vf[2];
+  auto kload = [&](int g) __attribute__((always_inline)) {  // K fragment of step g (0..8) into kf[g % 3]
+    const uint32_t a0 = g < 8 ? ka[2 * (g & 1)] + 128 * (g >> 1) : ka[4];
+    const uint32_t a1 = g < 8 ? ka[2 * (g & 1) + 1] + 128 * (g >> 1) : ka[5];
+    const v4i lo = *(const lds_v4i*)(uintptr_t)a0;
+    const v4i hi = *(const lds_v4i*)(uintptr_t)a1;
+    kf[g % 3] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  };
+  // V^T fragment of group g (dim tile dt = 8h + g) into vf[g % 2]
+  auto vload = [&](int h, int g) __attribute__((always_inline)) {
+    const int dt = 8 * h + g;
+    const uint32_t a0 = va[dt & 3] + 128 * (dt >> 2), a1 = va[4 + (dt & 3)] + 128 * (dt >> 2);
+    const v2i r0 = lds_read_tr8(a0);
+    const v2i r1 = lds_read_tr8(a1);
+    const v2i r2 = lds_read_tr8(a0 + C::TSTAGE);
+    const v2i r3 = lds_read_tr8(a1 + C::TSTAGE);
+    vf[g % 2] = v8i{r0[0], r0[1], r1[0], r1[1], r2[0], r2[1], r3[0], r3[1]};
+  };
+
+  v16f o[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) o[i] = v16f{};
+  float m_ref = 0.f, l_run = 0.f, m_seen = ninf();
+  bool have_ref = false, overflow = false;
+
+  // ---- softmax of tile t (scores s, one lane = one head, 16 tokens) ------------
+  // s[r] = raw score(token 8(r >> 2) + 4hh + (r & 3)); output: bytes 16u + 4q + i
+  // of the pair's P'^T B operands (u = t & 1: the tile's half) = the hi term
+  // (in w_hi) and the lo term (in w_lo) of token 8q + 4hh + i, and the tile's
+  // B scale (lane half u of wsc: the scale of K block u).  22 steps of a few
+  // VALU ops, one per MFMA slot.
+  v8i w_hi = v8i{}, w_lo = v8i{}, r_hi = v8i{}, r_lo = v8i{};  // P' being built / the PV operand
+  int wsc = 127, rsc = 127;
+  float mx = 0.f, sh = 0.f, ps = 0.f;  // tile max (then its clamped exponent), 8 - exponent, row sum
+  auto softmax_body = [&](auto K, auto U, int t, v16f& s, v8i& bh, v8i& bl) __attribute__((always_inline)) {
+    constexpr int u = decltype(U)::value;
+    constexpr int k = decltype(K)::value;
+    if constexpr (k == 0) {
+      asm volatile("s_nop 15" : "+v"(s));  // the tile's last QK MFMA (two slots back) has retired
+      const int nval = ntok - C::HT * t;
+      if (nval < C::HT) {  // token 8(r >> 2) + (r & 3) (+ 4hh) >= nval: a constant vs the lane limit
+        const int lim = nval - 4 * hh;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[r] = mask_ge(s[r], 8 * (r >> 2) + (r & 3), lim);
+      }
+      mx = max3f(max3f(s[0], s[1], s[2]), max3f(s[3], s[4], s[5]), s[6]);
+      mx = max3f(mx, s[7], s[8]);
+    } else if constexpr (k == 1) {
+      mx = max3f(max3f(mx, s[9], s[10]), max3f(s[11], s[12], s[13]), max3f(s[14], s[15], s[15]));
+    } else if constexpr (k == 2) {
+      mx = __builtin_ceilf(xhalf_max(mx) * c);  // the tile's ceil max (finite: every tile holds a token)
+    } else if constexpr (k == 3) {
+      if (!have_ref) {
+        m_ref = mx;
+        have_ref = true;
+      }
+      m_seen = fmaxf(m_seen, mx);
+      overflow = overflow || mx > m_ref + kRebaseF;
+      mx = fminf(mx, m_ref + kRebaseF);  // the exponent, clamped: a flagged pass is run again
+    } else if constexpr (k == 4) {
+      const int psc = min(max((int)fmaxf(mx - m_ref, -160.f) - 8 + 127, 0), 254);
+      if constexpr (u == 0) wsc = psc;
+      else wsc = hh ? psc : wsc;
+      sh = 8.f - mx;
+      ps = 0.f;
+    } else if constexpr (k <= 12) {  // P' = 2^(c s - m_t + 8) of two scores (at most 2^8 unless flagged)
+      constexpr int r = 2 * (k - 5);
+      s[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], c, sh));
+      s[r + 1] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r + 1], c, sh));
+      if constexpr (r > 0) ps += s[r - 2] + s[r - 1];  // the previous step's pair (no transcendental wait)
+    } else if constexpr (k == 13) {
+      ps += s[14] + s[15];
+      l_run = __builtin_fmaf(ps, __builtin_amdgcn_exp2f(fmaxf(mx - m_ref, -160.f) - 8.f), l_run);
+    } else {  // steps 14..21: quad qd, hi term then lo term (the hi codes decoded again)
+      constexpr int qd = (k - 14) / 2;
+      if constexpr ((k - 14) % 2 == 0) {
+        bh[4 * u + qd] = (int)pack4_fp8(s[4 * qd], s[4 * qd + 1], s[4 * qd + 2], s[4 * qd + 3]);
+      } else {
+        const v2f h01 = __builtin_amdgcn_cvt_pk_f32_fp8(bh[4 * u + qd], false);
+        const v2f h23 = __builtin_amdgcn_cvt_pk_f32_fp8(bh[4 * u + qd], true);
+        bl[4 * u + qd] = (int)pack4_fp8(s[4 * qd] - h01[0], s[4 * qd + 1] - h01[1], s[4 * qd + 2] - h23[0],
+                                          s[4 * qd + 3] - h23[1]);
+      }
+    }
+  };
+  auto softmax_step = [&](auto K, auto U, int t, v16f& s, v8i& bh, v8i& bl) __attribute__((always_inline)) {
+    // register fences: the step's work stays in its slot (neither hoisted
+    // above the previous MFMA nor sunk below the next)
+    asm volatile("" : "+v"(s), "+v"(mx), "+v"(l_run), "+v"(ps), "+v"(sh));
+    softmax_body(K, U, t, s, bh, bl);
+    asm volatile("" : "+v"(s), "+v"(bh), "+v"(bl), "+v"(mx), "+v"(l_run), "+v"(ps), "+v"(sh));
+  };
+
+  // ---- one pair of iterations -------------------------------------------------
+  // iteration t = 2q + IT: QK(t) | softmax(t - 1) | half IT ^ 1 of the PV of pair
+  // q - 2 + IT (dims 256 (1 - IT) .. +255: the pair's second half in iteration
+  // 0, the next pair's first half in iteration 1), a PV pair being the 64
+  // tokens of its two tiles, whose softmax ended the iteration before.
+  v16f sa, sb;  // QK accumulators of tiles of parity 0 / 1
+  int rs[2] = {0, 0};  // slots of the next row DMAs (read two slots ahead)
+  // GUARD: a pair at an edge of the pipeline, whose QK, softmax and PV parts
+  // run only where their tile (pair) exists: t < n; 1 <= t <= n; pair j >= 0,
+  // 2j < n.  Fragment loads and slot-index DMAs run everywhere (their
+  // addresses stay inside the ring and the item).  DM: the rows of pair q + 2
+  // (which exist iff q + 2 < npair) are fetched always (1), never (0), or as
+  // that test says (2).
+  auto pair = [&](auto guard_tag, auto dm_tag, int q) __attribute__((always_inline)) {
+    constexpr bool GUARD = decltype(guard_tag)::value;
+    constexpr int DM = decltype(dm_tag)::value;
+    asm volatile("" : "+s"(q));  // nothing that depends on q is precomputed (and kept live) outside the pair
+    const bool dmas = DM == 1 || (DM == 2 && q + 2 < npair);
+    const uint32_t stw = stage_of(q + 2), sring = sring_of(q + 2);
+    static_for<0, 2 * SC::kSlots>([&](auto S) __attribute__((always_inline)) {
+      constexpr int ps_ = decltype(S)::value;  // slot of the pair
+      constexpr int IT = ps_ / SC::kSlots;      // iteration of the pair (tile t = 2q + IT)
+      constexpr int i = ps_ % SC::kSlots;       // slot of the iteration
+      constexpr int H = 1 - IT;                 // PV half of the iteration
+      const int t = 2 * q + IT;
+      const int j = q - 2 + IT;                 // PV pair of the iteration
+      v16f& s_qk = IT == 0 ? sa : sb;  // tile t
+      v16f& s_sm = IT == 0 ? sb : sa;  // tile t - 1
+      // 0. the built P' (pair q - 1) becomes the PV operand
+      if constexpr (ps_ == SC::kCopy) {
+        r_hi = w_hi;
+        r_lo = w_lo;
+        rsc = wsc;
+      }
+      // 1. the slot's MFMA
+      if constexpr (SC::is_qk(i)) {
+        constexpr int g = i / 3;
+        if (!GUARD || t < n) {
+          if constexpr (g == 0) qk_first(s_qk, kf[0], qv[0]);
+          else qk_acc(s_qk, kf[g % 3], qv[g]);
+        }
+      } else {
+        constexpr int g = i / 3, term = i % 3 - 1;
+        if (!GUARD || (j >= 0 && 2 * j < n)) pv_mfma(o[8 * H + g], vf[g % 2], term == 0 ? r_hi : r_lo, rsc);
+      }
+      // 2. barriers: pair q - 2's stage free (every wave's last V^T read of it
+      // done); pair q + 1 published (its rows landed)
+      if constexpr (ps_ == SC::kStageFree) lds_barrier();
+      if constexpr (ps_ == SC::kBarrier) {
+        if constexpr (DM == 1) {
+          wait_rows();
+        } else if constexpr (DM == 0) {
+          wait_rows_last();
+        } else {
+          if (dmas) wait_rows();
+          else wait_rows_last();
+        }
+        lds_barrier();
+      }
+      // 3. slot indices of pair q + 4, rows of pair q + 2
+      if constexpr (ps_ == SC::kSlotDma) issue_slots(q + 4);
+      if constexpr (SC::row_dma(ps_) >= 0) {
+        constexpr int k = SC::row_dma(ps_);
+        if (dmas) row_dma(k, rs[k % 2], stw);
+      }
+      if constexpr (SC::row_read(ps_) >= 0) {
+        constexpr int k = SC::row_read(ps_);
+        if constexpr (DM != 0) rs[k % 2] = row_slot(k, q + 2, sring);
+      }
+      // 4. fragment loads, address moves
+      if constexpr (SC::kload(i) >= 0) kload(SC::kload(i) % 9);
+      if constexpr (SC::vload(i) >= 0) {
+        constexpr int g = SC::vload(i);
+        if constexpr (g < 8) vload(H, g);
+        else vload(IT, 0);  // group 0 of the next iteration (half IT ^ 1 ^ 1)
+      }
+      if constexpr (i == SC::kRebaseK) {
+        const int dk = IT == 0 ? C::TSTAGE : (((q + 1) & 3) - (q & 3)) * C::PSTAGE - C::TSTAGE;
+#pragma unroll
+        for (int jj = 0; jj < 6; ++jj) {
+          ka[jj] += dk;
+          asm volatile("" : "+v"(ka[jj]));
+        }
+      }
+      if constexpr (IT == 0 && i == SC::kRebaseV) {  // pair q - 2 -> q - 1
+        const int dv = (((q - 1) & 3) - ((q - 2) & 3)) * C::PSTAGE;
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) {
+          va[jj] += dv;
+          asm volatile("" : "+v"(va[jj]));
+        }
+      }
+      // 5. one softmax step of tile t - 1 (a tile past the item leaves its half
+      // of the operand zero)
+      if constexpr (i >= 2 && i < 2 + SC::kSoftSteps) {
+        if (!GUARD || (t >= 1 && t <= n)) {
+          softmax_step(Ic<i - 2>{}, Ic<1 - IT>{}, t - 1, s_sm, w_hi, w_lo);
+        } else if constexpr (i == 2) {
+#pragma unroll
+          for (int qd = 0; qd < 4; ++qd) {
+            w_hi[4 * (1 - IT) + qd] = 0;
+            w_lo[4 * (1 - IT) + qd] = 0;
+          }
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  };
+  const std::true_type Y{};
+  const std::false_type N{};
+  const Ic<0> Z{};
+  const Ic<1> A{};
+  const Ic<2> R{};
+
+  bool first = true;
+  for (;;) {
+    if (n > 0) {
+      // prologue: slots(0), slots(1) (and Q on the first pass); then what pair
+      // -1 would have issued (slots(2) before rows(0); slots(3) and rows(1) after)
+      issue_slots(0);
+      issue_slots(1);
+      if (first) {
+        issue_q();
+        if (IDX && w == 0) wait_vmcnt<kQWin>();  // the slot indices, not Q
+      } else {
+        wait_vmcnt<0>();
+      }
+      lds_barrier();
+      issue_slots(2);
+      issue_rows(0);
+      issue_slots(3);
+      issue_rows(1);
+      if (first) {  // this wave's Q rows landed (issued before the 20 or 22 DMAs since)
+        if (w == 0) wait_vmcnt<IDX ? 2 * C::DMAX + 2 : 2 * C::DMAX>();
+        else if (w == 1) wait_vmcnt<2 * C::DMAX>();
+        else wait_vmcnt<2 * C::DMAX - 2>();
+        read_q();
+      }
+      wait_rows();
+      lds_barrier();  // pair 0 visible; every wave's Q^T reads done (stage 2 reusable)
+      init_ka();
+      init_va();
+      kload(0);
+      kload(1);
+      vload(1, 0);
+      // pairs: the first two (pipeline fill), the steady ones (every part of
+      // both iterations runs: PV pairs q - 2 >= 0 and q - 1, QK tiles 2q + 1 < n),
+      // then those that drain the pipeline (the last PV pair, npair - 1, runs in
+      // pairs npair and npair + 1)
+      int q = 0;
+      pair(Y, R, 0);
+      pair(Y, R, 1);
+      for (q = 2; q + 2 < npair; ++q) pair(N, A, q);  // q + 2 < npair implies 2q + 1 < n
+      for (; 2 * q + 1 < n; ++q) pair(N, Z, q);
+      for (; q <= npair + 1; ++q) pair(Y, R, q);
+    }
+    // a flagged head on any wave: run the item again from the running maxima
+    wait_vmcnt<0>();
+    if (lane == 0) smem[C::OFF_FLAG + w] = __any(overflow) ? 1 : 0;
+    lds_barrier();
+    const bool again = __builtin_amdgcn_readfirstlane(*reinterpret_cast<const int*>(smem + C::OFF_FLAG)) != 0;
+    lds_barrier();  // flags read before anyone rewrites them
+    if (!again) break;
+    m_ref = m_seen;
+    overflow = false;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[i] = v16f{};
+    l_run = 0.f;
+    first = false;
+  }
+
+  // ---- finish: normalize, transpose O^T through LDS, coalesced row stores ------
+  asm volatile("s_nop 15\n\ts_nop 15" ::: "memory");  // last PV MFMAs retired before O^T is read
+  const float L = xhalf_sum(l_run);
+  const float inv = L > 0.f ? vscale / L : 0.f;
+  wait_vmcnt<0>();
+  lds_barrier();  // every wave done with the ring
+  // wave w's O^T tile -> bf16 [32 heads][512 dims] at 32.5 KiB w (rows of
+  // 1 KiB + 16 B against bank conflicts)
+  constexpr int ORST = 1040;
+  uint8_t* ob = smem + w * 32 * ORST;
+#pragma unroll
+  for (int dt = 0; dt < 16; ++dt) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int d = 32 * dt + 8 * q + 4 * hh;
+      const uint32_t lo = f32_to_bf16_bits(o[dt][4 * q] * inv) | (f32_to_bf16_bits(o[dt][4 * q + 1] * inv) << 16);
+      const uint32_t hi = f32_to_bf16_bits(o[dt][4 * q + 2] * inv) | (f32_to_bf16_bits(o[dt][4 * q + 3] * inv) << 16);
+      *reinterpret_cast<uint2*>(ob + l32 * ORST + 2 * d) = make_uint2(lo, hi);
+    }
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's rows written (only it reads them)
+  const float lse2 = L > 0.f ? m_ref + __log2f(L) : ninf();
+  uint16_t* dst = slot < 0 ? p.out + ((int64_t)b * 128 + 32 * w) * kVDim
+                           : p.part_o + ((int64_t)slot * 128 + 32 * w) * kVDim;
+#pragma unroll 8
+  for (int h = 0; h < 32; ++h) {
+    const uint4 v = *reinterpret_cast<const uint4*>(ob + h * ORST + 16 * lane);
+    *reinterpret_cast<uint4*>(dst + (int64_t)h * kVDim + 8 * lane) = v;
+  }
+  if (hh == 0) {
+    if (slot < 0) {
+      if (p.lse_out != nullptr) p.lse_out[(int64_t)b * 128 + head] = L > 0.f ? lse2 * kLn2F : ninf();
+    } else {
+      p.part_lse[(int64_t)slot * 128 + head] = lse2;
+    }
+  }
+}
+
+}  // namespace
+
+hipError_t launch_decode_h128f(const DecodeParams& p, int grid, hipStream_t stream) {
+  if (p.kv_indices != nullptr)
+    hipLaunchKernelGGL(decode_h128f_kernel<true>, dim3(grid), dim3(256), 0, stream, p);
+  else
+    hipLaunchKernelGGL(decode_h128f_kernel<false>, dim3(grid), dim3(256), 0, stream, p);
+  return hipGetLastError();
+}
+
+}  // namespace mla
