@@ -20,7 +20,7 @@ CSRC = os.path.join(PKG_DIR, "csrc")
 BUILD_DIR = os.path.join(PKG_DIR, "_build")
 LIB_NAME = "libmla_mi355x.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
-SOURCES = ["quant.hip", "decode.hip", "neighbours.hip", "selftest.hip", "abi.hip", "noalloc.hip", "probe.hip"]
+SOURCES = ["quant.hip", "decode.hip", "decode_h128.hip", "neighbours.hip", "selftest.hip", "abi.hip", "noalloc.hip", "probe.hip"]
 ARCH = os.environ.get("MLA_OFFLOAD_ARCH", "gfx950")
 
 # -packed-fp32-ops: keep the compiler from forming v_pk_{add,mul,fma}_f32
