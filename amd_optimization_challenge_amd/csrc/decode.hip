@@ -989,10 +989,10 @@ __global__ __launch_bounds__(256) void combine_kernel(const DecodeParams p) {
     uint4 v[8];  // 8 bf16 of split s0 + j
     float ls[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int s = min(s0 + j, bi.y - 1);
-      v[j] = *reinterpret_cast<const uint4*>(po + s * sstride);
-      ls[j] = s0 + j < bi.y ? lse[(int64_t)s * H] : neg_inf();
+    for (int j = 0; j < 8; ++j) {  // only the splits that exist are loaded
+      const bool ok = s0 + j < bi.y;
+      v[j] = ok ? *reinterpret_cast<const uint4*>(po + (s0 + j) * sstride) : make_uint4(0, 0, 0, 0);
+      ls[j] = ok ? lse[(int64_t)(s0 + j) * H] : neg_inf();
     }
     float mb = M;
 #pragma unroll
