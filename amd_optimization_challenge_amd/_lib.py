@@ -33,6 +33,7 @@ SIGNATURES = {
     "mla_pack_mxfp4": (_I, [_P, _L, _I, _L, _P, _L, _P, _L, _P]),
     "mla_append_kv": (_I, [_P, _L, _L, _P, _P, _L, _P, _P, _L, _P, _L, _P, _P]),
     "mla_plan": (_I, [_P, _I, _I, _I, _I, _P, _L, _P]),
+    "mla_expand_pages": (_I, [_P, _P, _P, _I, _I, _L, _P, _P, _P]),
     "mla_decode": (_I, [_P, _P, _P, _L, _P, _L, _P, _L, _P, _P, _P, _I, _I, _F, _I, _P, _L, _P, _P, _P]),
     "mla_combine": (_I, [_I, _I, _P, _L, _P, _P, _P]),
     "mla_decode_fwd": (_I, [_P, _P, _L, _P, _L, _P, _L, _P, _P, _P, _I, _I, _I, _F, _I, _P, _L, _P, _P, _P]),

@@ -280,6 +280,24 @@ int mla_append_kv(const void* x_bf16, int64_t n, int64_t x_row_stride, const int
   return MLA_OK;
 }
 
+int mla_expand_pages(const int32_t* page_indptr, const int32_t* page_ids, const int32_t* last_page_lens,
+                     int batch, int page_size, int64_t max_pages, int32_t* kv_indptr_out,
+                     int32_t* kv_indices_out, void* stream) {
+  if (batch < 1) return set_error(MLA_ERR_INVALID_ARGUMENT, "batch must be >= 1 (got %d)", batch);
+  if (page_size < 1 || page_size > 65536)
+    return set_error(MLA_ERR_INVALID_ARGUMENT, "page_size must be in [1, 65536] (got %d)", page_size);
+  if (max_pages < 0 || max_pages * (int64_t)page_size >= (int64_t(1) << 31))
+    return set_error(MLA_ERR_INVALID_ARGUMENT,
+                     "max_pages * page_size must stay below 2^31 token rows (got %lld x %d)",
+                     (long long)max_pages, page_size);
+  if (!page_indptr || !last_page_lens || !kv_indptr_out || (max_pages > 0 && (!page_ids || !kv_indices_out)))
+    return set_error(MLA_ERR_INVALID_ARGUMENT, "null pointer argument");
+  hipError_t e = launch_expand_pages(page_indptr, page_ids, last_page_lens, batch, page_size, max_pages,
+                                     kv_indptr_out, kv_indices_out, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "expand_pages launch");
+  return MLA_OK;
+}
+
 int mla_plan(const int32_t* kv_indptr, int batch, int q_seq_len, int num_heads, int kv_mode, void* workspace,
              int64_t workspace_bytes, void* stream) {
   int rc = check_shape(batch, num_heads, kv_mode);

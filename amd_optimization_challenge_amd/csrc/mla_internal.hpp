@@ -48,6 +48,9 @@ hipError_t launch_pack_mxfp4(const uint16_t* x, int64_t rows, int cols, int64_t 
                              int64_t scale_stride, hipStream_t stream);
 hipError_t launch_plan(const int32_t* kv_indptr, int batch, int qlen, int target_items, int max_items,
                        int32_t* plan, hipStream_t stream);
+hipError_t launch_expand_pages(const int32_t* page_indptr, const int32_t* page_ids, const int32_t* last_page_lens,
+                               int batch, int page_size, int64_t max_pages, int32_t* kv_indptr_out,
+                               int32_t* kv_indices_out, hipStream_t stream);
 hipError_t launch_append_kv(const uint16_t* x, int64_t n, int64_t x_stride, const int32_t* slots,
                             uint8_t* fp8_cache, int64_t fp8_stride, const float* fp8_scale,
                             uint8_t* fp4_cache, int64_t fp4_stride, uint8_t* fp4_scales,

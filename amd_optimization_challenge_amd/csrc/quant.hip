@@ -507,6 +507,64 @@ __global__ __launch_bounds__(256) void plan_kernel(const int32_t* __restrict__ k
 }
 
 // ---------------------------------------------------------------------------
+// Paged caches: AITER's page table (kv_indptr over pages, page ids,
+// kv_last_page_lens, page_size; mixed-mla/asm_dumps/aiter_mla.py:149-175, built
+// as at mixed-mla/submission.py:449-456 and :538-544) expanded into the
+// token-level kv_indptr / kv_indices every decode kernel reads.  Sequence b
+// holds n_b = indptr[b+1] - indptr[b] pages and L_b = (n_b - 1) P + last_b
+// tokens (0 when n_b = 0; last_b clamped to [1, P]); its token j is row
+// page_ids[indptr[b] + j / P] * P + j % P of the flattened [pages * P, row]
+// cache.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int paged_len(const int32_t* __restrict__ page_indptr,
+                                         const int32_t* __restrict__ last_page_lens, int b, int P) {
+  const int np = page_indptr[b + 1] - page_indptr[b];
+  return np > 0 ? (np - 1) * P + min(max(last_page_lens[b], 1), P) : 0;
+}
+
+// one block: token counts of every sequence, exclusive scan -> kv_indptr_out
+__global__ __launch_bounds__(256) void paged_indptr_kernel(const int32_t* __restrict__ page_indptr,
+                                                           const int32_t* __restrict__ last_page_lens,
+                                                           int batch, int P, int32_t* __restrict__ kv_indptr_out) {
+  __shared__ int red[4];
+  int carry = 0;
+  for (int base = 0; base < batch; base += 256) {
+    const int b = base + (int)threadIdx.x;
+    const int L = b < batch ? paged_len(page_indptr, last_page_lens, b, P) : 0;
+    int tot = 0;
+    const int ex = block_exscan(L, red, &tot);
+    if (b < batch) kv_indptr_out[b] = carry + ex;
+    carry += tot;
+  }
+  if (threadIdx.x == 0) kv_indptr_out[batch] = carry;
+}
+
+// one thread per page: its sequence by binary search over the page indptr,
+// then its up-to-P token rows
+__global__ __launch_bounds__(256) void paged_indices_kernel(const int32_t* __restrict__ page_indptr,
+                                                            const int32_t* __restrict__ page_ids,
+                                                            const int32_t* __restrict__ last_page_lens,
+                                                            int batch, int P, int64_t max_pages,
+                                                            const int32_t* __restrict__ kv_indptr,
+                                                            int32_t* __restrict__ kv_indices_out) {
+  const int64_t pg = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (pg >= max_pages || pg >= page_indptr[batch]) return;
+  int lo = 0, hi = batch - 1;  // last b with page_indptr[b] <= pg
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (page_indptr[mid] <= pg) lo = mid;
+    else hi = mid - 1;
+  }
+  const int b = lo;
+  const int j = (int)(pg - page_indptr[b]);
+  const int np = page_indptr[b + 1] - page_indptr[b];
+  const int cnt = j == np - 1 ? min(max(last_page_lens[b], 1), P) : P;
+  const int32_t row0 = page_ids[pg] * P;
+  int32_t* dst = kv_indices_out + kv_indptr[b] + (int64_t)j * P;
+  for (int i = 0; i < cnt; ++i) dst[i] = row0 + i;
+}
+
+// ---------------------------------------------------------------------------
 // host launchers
 // ---------------------------------------------------------------------------
 static int amax_blocks_for(int64_t n) {
@@ -562,6 +620,19 @@ hipError_t launch_append_kv(const uint16_t* x, int64_t n, int64_t x_stride, cons
   hipLaunchKernelGGL(append_kv_kernel, dim3((int)g), dim3(256), 0, stream,
                      reinterpret_cast<const uint8_t*>(x), (int)n, x_stride, slots, fp8_cache, fp8_stride,
                      fp8_scale, fp4_cache, fp4_stride, fp4_scales, fp4_scale_stride, amax_out);
+  return hipGetLastError();
+}
+
+hipError_t launch_expand_pages(const int32_t* page_indptr, const int32_t* page_ids, const int32_t* last_page_lens,
+                               int batch, int page_size, int64_t max_pages, int32_t* kv_indptr_out,
+                               int32_t* kv_indices_out, hipStream_t stream) {
+  hipLaunchKernelGGL(paged_indptr_kernel, dim3(1), dim3(256), 0, stream, page_indptr, last_page_lens, batch,
+                     page_size, kv_indptr_out);
+  if (max_pages > 0) {
+    const int64_t g = (max_pages + 255) / 256;
+    hipLaunchKernelGGL(paged_indices_kernel, dim3((unsigned)g), dim3(256), 0, stream, page_indptr, page_ids,
+                       last_page_lens, batch, page_size, max_pages, kv_indptr_out, kv_indices_out);
+  }
   return hipGetLastError();
 }
 

@@ -183,25 +183,56 @@ def append_kv(x: torch.Tensor, slots: torch.Tensor | None, fp8=None, mxfp4=None,
 # ---------------------------------------------------------------------------
 
 
+def _rows(x: torch.Tensor) -> torch.Tensor:
+    """The cache as [rows, bytes per row]: every leading dimension (tokens, or
+    pages x page_size x kv heads of a paged cache) flattened into rows."""
+    x = as_bytes(x)
+    return x if x.dim() == 2 else x.flatten(0, x.dim() - 2)
+
+
 def _kv_args(kv_mode: int, kv_data: dict):
     """(k_cache, k_row_stride, k_scales, k_scale_stride, v_cache, v_row_stride, kv_scale)."""
     if kv_mode == 0:
         fp8, sc = kv_data["fp8"]
-        k = as_bytes(fp8).reshape(fp8.shape[0], -1)
+        k = _rows(fp8)
         return k, k.stride(0), None, 0, None, 0, sc
     if kv_mode == 1:
         fp4, e8 = kv_data["mxfp4"]
-        k = as_bytes(fp4).reshape(fp4.shape[0], -1)
-        s = as_bytes(e8)
+        k = _rows(fp4)
+        s = _rows(e8)
         return k, k.stride(0), s, s.stride(0), None, 0, None
     if kv_mode == 2:
         fp4, e8 = kv_data["mxfp4"]
         fp8, sc = kv_data["fp8"]
-        k = as_bytes(fp4).reshape(fp4.shape[0], -1)
-        s = as_bytes(e8)
-        v = as_bytes(fp8).reshape(fp8.shape[0], -1)
+        k = _rows(fp4)
+        s = _rows(e8)
+        v = _rows(fp8)
         return k, k.stride(0), s, s.stride(0), v, v.stride(0), sc
     raise ValueError(kv_mode)
+
+
+def expand_pages(page_indptr: torch.Tensor, page_ids: torch.Tensor, last_page_lens: torch.Tensor,
+                 page_size: int):
+    """AITER's page table -> the token-level (kv_indptr, kv_indices) over the
+    cache viewed as [pages * page_size, row] (``mla_expand_pages``).
+    kv_indices has room for every page full; entries past kv_indptr[-1] are
+    not written."""
+    _require_cuda(page_indptr, page_ids, last_page_lens)
+    for name, t in (("page_indptr", page_indptr), ("page_ids", page_ids), ("last_page_lens", last_page_lens)):
+        if t.dtype != torch.int32 or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous int32 tensor")
+    batch = page_indptr.numel() - 1
+    if batch < 1 or last_page_lens.numel() != batch:
+        raise ValueError("page_indptr needs batch + 1 entries and last_page_lens batch entries")
+    page_size = int(page_size)
+    max_pages = page_ids.numel()
+    kv_indptr = torch.empty(batch + 1, dtype=torch.int32, device=page_indptr.device)
+    kv_indices = torch.empty(max(max_pages * page_size, 1), dtype=torch.int32, device=page_indptr.device)
+    with torch.cuda.device(page_indptr.device):
+        _lib.check(_lib.load().mla_expand_pages(
+            _ptr(page_indptr), _ptr(page_ids), _ptr(last_page_lens), batch, page_size, max_pages,
+            _ptr(kv_indptr), _ptr(kv_indices), _stream()), "mla_expand_pages")
+    return kv_indptr, kv_indices
 
 
 def plan(kv_indptr: torch.Tensor, batch: int, num_heads: int, kv_mode, ws: torch.Tensor,
@@ -231,14 +262,20 @@ def combine(batch: int, num_heads: int, ws: torch.Tensor, out: torch.Tensor, lse
 
 
 def decode_fwd(q, kv_data, kv_indptr, kv_indices, sm_scale, kv_mode="fp8", out=None, ws=None, q_seq_len=1,
-               return_lse=False):
+               return_lse=False, page_size=1, kv_last_page_lens=None):
     """Whole operator: FP8-quantize q, plan, decode, combine.
 
     q: bf16 [rows, H, 576], rows = sequences x q_seq_len (row i of a sequence
     attends causally to its first L - (q_seq_len - 1 - i) keys).  Returns the
     bf16 [rows, H, 512] output, plus the f32 [rows, H] natural-log lse when
-    ``return_lse``.
+    ``return_lse``.  page_size > 1: a paged cache as AITER's mla_decode_fwd
+    takes it (caches [pages, page_size, 1, row], kv_indptr over pages,
+    kv_indices = page ids, kv_last_page_lens), expanded on the device first.
     """
+    if int(page_size) != 1:
+        if kv_indices is None or kv_last_page_lens is None:
+            raise ValueError("a paged cache needs kv_indices (page ids) and kv_last_page_lens")
+        kv_indptr, kv_indices = expand_pages(kv_indptr, kv_indices, kv_last_page_lens, page_size)
     _require_cuda(q, kv_indptr, kv_indices)
     if q.dtype != torch.bfloat16 or q.dim() != 3 or q.shape[-1] != QK_DIM:
         raise ValueError("q must be bf16 [rows, heads, 576]")

@@ -11,8 +11,11 @@ reference's causal multi-token decode (uniform qo length,
 competitor_submissions/mi355x_reference/reference.py:188-193; ``qo_indptr``
 is taken to be ``arange * q_seq_len`` as generate_input makes it, :330), and
 ``config["return_lse"]`` also returns the f32 log-sum-exp
-(mixed-mla/asm_dumps/aiter_mla.py:367-371).  There is no fallback: a missing
-library or an unsupported shape raises.
+(mixed-mla/asm_dumps/aiter_mla.py:367-371).  ``config["page_size"] > 1`` takes
+a paged cache the way AITER's mla_decode_fwd does (aiter_mla.py:149-175): the
+caches shaped [pages, page_size, 1, row], ``kv_indptr`` over pages,
+``config["kv_indices"]`` the page ids and ``config["kv_last_page_lens"]``.
+There is no fallback: a missing library or an unsupported shape raises.
 """
 from __future__ import annotations
 
@@ -39,5 +42,7 @@ def custom_kernel(data: input_t) -> output_t:
         raise ValueError("q.shape[0] must equal batch * q_seq_len")
     if qo_indptr is not None and qo_indptr.numel() != kv_indptr.numel():
         raise ValueError("qo_indptr and kv_indptr must both have batch + 1 entries")
+    page_size = int(config.get("page_size", 1))
     return ops.decode_fwd(q, kv_data, kv_indptr, kv_indices, sm_scale, kv_mode, q_seq_len=q_seq_len,
-                          return_lse=bool(config.get("return_lse", False)))
+                          return_lse=bool(config.get("return_lse", False)), page_size=page_size,
+                          kv_last_page_lens=config.get("kv_last_page_lens"))

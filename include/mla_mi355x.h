@@ -133,6 +133,22 @@ int mla_append_kv(const void* x_bf16, int64_t n, int64_t x_row_stride, const int
                   void* stream);
 
 /*
+ * Paged caches.  Expands AITER's page table -- page_indptr [batch + 1] over
+ * pages, page_ids (page index per page slot), last_page_lens [batch] and
+ * page_size, the arguments of mla_decode_fwd at
+ * mixed-mla/asm_dumps/aiter_mla.py:149-175 (built as at
+ * mixed-mla/submission.py:449-456, :538-544) -- into the token-level
+ * kv_indptr_out [batch + 1] and kv_indices_out (at most max_pages * page_size
+ * entries) that every decode entry point takes, addressing the cache viewed as
+ * [pages * page_size, row].  Sequence b holds (n_b - 1) * page_size + last_b
+ * tokens for n_b > 0 pages (last_b clamped to [1, page_size]).  max_pages is
+ * the length of page_ids; page_ids * page_size must stay below 2^31.
+ */
+int mla_expand_pages(const int32_t* page_indptr, const int32_t* page_ids, const int32_t* last_page_lens,
+                     int batch, int page_size, int64_t max_pages, int32_t* kv_indptr_out,
+                     int32_t* kv_indices_out, void* stream);
+
+/*
  * Split-KV work partition, computed on the device from kv_indptr (no host
  * sync).  Replaces get_mla_metadata_v1
  * (competitor_submissions/mi355x_reference/reference.py:161-209) and the

@@ -27,6 +27,11 @@ task files):
 * ``mla_decode``               -- the dequantize-then-fp32
   softmax(Q K^T * sm_scale) V that ``ref_kernel`` (TASK/reference.py:349-369)
   approximates through AITER, gathered through ``kv_indices`` (page size 1).
+* ``expand_pages`` / ``page_table`` -- AITER's paged-cache arguments
+  (kv_indptr over pages, page ids, kv_last_page_lens, page_size;
+  mixed-mla/asm_dumps/aiter_mla.py:149-175) as the reference builds them from
+  per-sequence token counts (mixed-mla/submission.py:449-456, :538-544), and
+  their expansion to the token rows of the cache viewed as [pages * P, row].
 * ``absorb_q`` / ``v_up_proj``  -- the neighbouring per-head products the
   reference names but does not implement (mixed-mla/README.md:213-217): the
   W_UK absorption that produces the decode's 576-wide Q and the v_up_proj
@@ -50,6 +55,9 @@ Parity pins (see tests/test_oracle_*.py):
                  identical keys), permutation/split invariance.
   neighbours  -- float64 brute force on tiny shapes; identity-block weights
                  reproduce the input columns; the rope columns pass through.
+  paging      -- page_table then expand_pages returns every token's row (a
+                 round trip through a random page placement); page_size 1 is
+                 the identity.
 """
 from __future__ import annotations
 
@@ -329,6 +337,43 @@ def dequant_kv(kv_mode: str, fp8_codes=None, fp8_scale=None, fp4_packed=None,
         v = dequant_fp8(fp8_codes.reshape(-1, QK_DIM), fp8_scale)[:, :V_DIM]
         return k, v
     raise ValueError(kv_mode)
+
+
+def page_table(lengths, page_size, page_ids_for):
+    """Per-sequence token counts -> AITER's page table, as mixed-mla/submission.py
+    :449-456 and :538-544 build it: ceil(L / P) pages per sequence, last-page
+    length L % P (P when 0).  ``page_ids_for(b, n)`` chooses the n page ids of
+    sequence b.  Returns (page_indptr [B+1], page_ids, last_page_lens [B]) int32.
+    """
+    P = int(page_size)
+    npages = [(int(L) + P - 1) // P for L in lengths]
+    indptr = np.concatenate([[0], np.cumsum(npages)]).astype(np.int32)
+    ids = np.concatenate([np.asarray(page_ids_for(b, n), dtype=np.int64) for b, n in enumerate(npages)] +
+                         [np.zeros(0, np.int64)]).astype(np.int32)
+    last = np.array([(int(L) % P) or P for L in lengths], dtype=np.int32)
+    return indptr, ids, last
+
+
+def expand_pages(page_indptr, page_ids, last_page_lens, page_size):
+    """AITER's page table -> token-level (kv_indptr [B+1], kv_indices [T]) over
+    the cache viewed as [pages * P, row]: sequence b has (n_b - 1) P + last_b
+    tokens for n_b > 0 pages (last_b clamped to [1, P]); its token j is row
+    page_ids[indptr[b] + j // P] * P + j % P (aiter_mla.py:149-175 with the
+    kv_buffer [pages, page, 1, 576] view of mixed-mla/submission.py:508-509)."""
+    P = int(page_size)
+    indptr = np.asarray(page_indptr, dtype=np.int64)
+    ids = np.asarray(page_ids, dtype=np.int64)
+    last = np.asarray(last_page_lens, dtype=np.int64)
+    lens, rows = [], []
+    for b in range(len(indptr) - 1):
+        n = int(indptr[b + 1] - indptr[b])
+        L = (n - 1) * P + min(max(int(last[b]), 1), P) if n > 0 else 0
+        lens.append(L)
+        j = np.arange(L, dtype=np.int64)
+        rows.append(ids[indptr[b] + j // P] * P + j % P)
+    kv_indptr = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    kv_indices = np.concatenate(rows + [np.zeros(0, np.int64)]).astype(np.int32)
+    return kv_indptr, kv_indices
 
 
 def row_ranges(kv_indptr, q_seq_len=1):

@@ -66,6 +66,12 @@ def test_argument_errors_without_device():
     assert lib.mla_plan(None, 6, 4, 16, 0, None, 0, None) == _lib.MLA_ERR_INVALID_ARGUMENT
     assert lib.mla_decode_fwd(None, None, 576, None, 0, None, 0, None, None, None, 6, 4, 16, 0.1, 0, None, 0,
                               None, None, None) == _lib.MLA_ERR_INVALID_ARGUMENT
+    # page-table expansion: bad batch / page size, 2^31-row overflow, null pointers
+    assert lib.mla_expand_pages(None, None, None, 0, 16, 0, None, None, None) == _lib.MLA_ERR_INVALID_ARGUMENT
+    assert lib.mla_expand_pages(None, None, None, 4, 0, 0, None, None, None) == _lib.MLA_ERR_INVALID_ARGUMENT
+    assert lib.mla_expand_pages(16, 16, 16, 4, 64, 1 << 25, 16, 16, None) == _lib.MLA_ERR_INVALID_ARGUMENT
+    assert b"2^31" in lib.mla_last_error()
+    assert lib.mla_expand_pages(None, None, None, 4, 8, 10, None, None, None) == _lib.MLA_ERR_INVALID_ARGUMENT
     # the no-alloc variant: stated scratch size, shape errors before any device call
     assert lib.mla_noalloc_scratch_bytes() == 64 << 20
     assert lib.mla_decode_fwd_noalloc(None, None, 576, None, 0, None, 0, None, None, None, 4, 1, 24, 0.1, 0,
