@@ -411,6 +411,46 @@ int mla_decode_fwd(const void* q_bf16, const void* k_cache, int64_t k_row_stride
   return MLA_OK;
 }
 
+int mla_decode_fwd_a16w8(const void* q_bf16, const void* k_cache, int64_t k_row_stride, const void* k_scales,
+                         int64_t k_scale_stride, const void* v_cache, int64_t v_row_stride,
+                         const float* kv_scale, const int32_t* kv_indptr, const int32_t* kv_indices, int batch,
+                         int q_seq_len, int num_heads, float sm_scale, int kv_mode, void* workspace,
+                         int64_t workspace_bytes, void* out_bf16, float* lse_out, void* stream) {
+  if (num_heads != 16 || kv_mode != 0)
+    return set_error(MLA_ERR_UNSUPPORTED, "the a16w8 route takes 16 heads and the fp8 cache (got %d, kv_mode %d)",
+                     num_heads, kv_mode);
+  if (!q_bf16 || !aligned(q_bf16, 16)) return set_error(MLA_ERR_INVALID_ARGUMENT, "q must be non-null and 16-byte aligned");
+  if (!workspace) return set_error(MLA_ERR_INVALID_ARGUMENT, "null workspace");
+  int rc = check_shape(batch, num_heads, kv_mode);
+  if (rc) return rc;
+  if ((rc = check_qlen(batch, q_seq_len))) return rc;
+  int ncu = 0;
+  if ((rc = cu_count(&ncu))) return rc;
+  WsLayout L0 = workspace_layout(batch, num_heads, kv_mode, ncu);
+  if (workspace_bytes < L0.total)
+    return set_error(MLA_ERR_WORKSPACE_TOO_SMALL, "workspace needs %lld bytes (got %lld)", (long long)L0.total,
+                     (long long)workspace_bytes);
+  char* ws = static_cast<char*>(workspace);
+  DecodeParams p;
+  WsLayout L;
+  // the fp8 Q slots of the workspace are not read on this route
+  rc = decode_params(ws + L0.qfp8_off, reinterpret_cast<const float*>(ws + L0.quant_off + 4096), k_cache,
+                     k_row_stride, k_scales, k_scale_stride, v_cache, v_row_stride, kv_scale, kv_indptr,
+                     kv_indices, batch, num_heads, sm_scale, kv_mode, workspace, workspace_bytes, out_bf16,
+                     lse_out, &p, &L);
+  if (rc) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e = launch_plan(kv_indptr, batch, q_seq_len, target_items_for(batch, num_heads, kv_mode, ncu),
+                             L.max_items, reinterpret_cast<int32_t*>(ws + L.plan_off), s);
+  if (e != hipSuccess) return hip_fail(e, "plan launch");
+  p.q_bf16 = static_cast<const uint16_t*>(q_bf16);  // no partials: each work-group scales its own Q rows
+  e = launch_decode(p, kv_mode, L.max_items, s);
+  if (e != hipSuccess) return hip_fail(e, "decode launch");
+  e = launch_combine(p, s);
+  if (e != hipSuccess) return hip_fail(e, "combine launch");
+  return MLA_OK;
+}
+
 int mla_absorb_q(const void* q_nope, const void* q_rope, const void* w_uk, int batch, int num_heads,
                  void* q_out, void* stream) {
   if (batch < 1 || num_heads < 1 || num_heads > 65535)

@@ -156,9 +156,17 @@ struct H16 {
 constexpr int kVScaleSpan = 31;  // fp4 V: P' = P 2^(e - E_ref) <= 2^(96 + 31) stays finite in bf16
 
 
-template <int KF, int VF, bool IDX, bool QB>
+// QM: how Q arrives.  0: fp8 codes and their per-tensor scale (the staged
+// path).  1: bf16, quantized here per tensor from the amax partials (a8w8).
+// 2: bf16 with no tensor-wide scale (a16w8, fp8 K only): each head row is
+// split here into two fp8 terms at a power-of-two row scale 2^e, hi =
+// e4m3(q 2^-e) and lo = e4m3((q 2^-e - hi) 2^4), and QK runs one MFMA per term
+// (the lo one with B scale 2^-4), about 8 significant bits of Q as bf16 has.
+template <int KF, int VF, bool IDX, int QM>
 __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_kernel(const DecodeParams p) {
   using C = H16<KF, VF>;
+  constexpr bool QB = QM != 0;
+  static_assert(QM != 2 || KF == 0, "a16w8: fp8 K only");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[C::LDS];
   const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
 
@@ -274,6 +282,7 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
   // g' where 32g + e = 16g' + (i & 15) + 64 (i >> 4); the fp8 Q operand is
   // gathered in that order.  With fp8 K both operands share one order.
   v8i qv[5];
+  v8i qlo[QM == 2 ? 5 : 1];  // a16w8: the lo term of Q
   float c = 0.f;  // qs * kv scale (fp8 K) * sm_scale * log2(e), set once Q is resident
   const float kvs = (KF == 0 || VF == 1) ? p.kv_scale[0] : 1.0f;
   const float vscale = VF == 2 ? 1.0f : kvs;
@@ -307,13 +316,79 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
   if constexpr (QB) {
     const uint8_t* src = reinterpret_cast<const uint8_t*>(p.q_bf16 + (int64_t)b * 16 * kQKDim);
     for (int k = w; k < QNV / 64; k += 4) dma16_to_lds(src + 1024 * k + 16 * lane, qlds + 1024 * k);
-    for (int i = tid; i < p.q_nparts; i += 256) qm = max(qm, p.q_partials[i]);
+    if constexpr (QM == 1)
+      for (int i = tid; i < p.q_nparts; i += 256) qm = max(qm, p.q_partials[i]);
   } else {
     load_q(p.q_fp8 + ((int64_t)b * 16 + l16) * kQKDim);
     c = p.q_scale[0] * (KF == 0 ? kvs : 1.0f) * p.sm_scale * kLog2e;
   }
   auto quantize_q = [&]() __attribute__((always_inline)) {  // block-uniform; the loads have landed
-    if constexpr (QB) {
+    if constexpr (QM == 2) {
+      // per head row: |q| max (bf16 bits) -> row exponent e (q 2^-e <= 448),
+      // then both terms written over the bf16 rows (hi at row r, lo 9 KiB on)
+      uint8_t* qst = smem + (C::S - 1) * C::STAGE;
+      uint32_t* rmax = reinterpret_cast<uint32_t*>(smem + C::OFF_X);  // [16] row maxima, then exponents
+      if (tid < 16) rmax[tid] = 0;
+      uint4 xv[QNJ];
+#pragma unroll
+      for (int j = 0; j < QNJ; ++j) {
+        const int i = tid + 256 * j;
+        if (i < QNV) xv[j] = *reinterpret_cast<const uint4*>(qst + 16 * i);
+      }
+      lds_barrier();  // rmax zeroed
+#pragma unroll
+      for (int j = 0; j < QNJ; ++j) {
+        const int i = tid + 256 * j;
+        if (i < QNV) {
+          const uint32_t wv[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
+          uint32_t m = 0;
+#pragma unroll
+          for (int k = 0; k < 4; ++k) m = max(m, max(wv[k] & 0x7FFFu, (wv[k] >> 16) & 0x7FFFu));
+          atomicMax(&rmax[i / (kQKDim / 8)], m);
+        }
+      }
+      lds_barrier();  // row maxima complete; every bf16 chunk read before the fp8 terms overwrite them
+      if (tid < 16) {
+        const float a = bf16_bits_to_f32(rmax[tid]);
+        int e = a > 0.f ? (int)__builtin_ceilf(__log2f(a * (1.0f / 448.0f))) : 0;
+        e = min(max(e, -126), 126);
+        if (a * __builtin_amdgcn_ldexpf(1.0f, -e) > 448.0f) ++e;  // log2 rounding
+        rmax[16 + tid] = (uint32_t)e;
+      }
+      lds_barrier();
+#pragma unroll
+      for (int j = 0; j < QNJ; ++j) {
+        const int i = tid + 256 * j;
+        if (i < QNV) {
+          const float sc = __builtin_amdgcn_ldexpf(1.0f, -(int)rmax[16 + i / (kQKDim / 8)]);
+          const uint32_t wv[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
+          float y[8];
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            y[2 * k] = bf16_bits_to_f32(wv[k] & 0xFFFFu) * sc;
+            y[2 * k + 1] = bf16_bits_to_f32(wv[k] >> 16) * sc;
+          }
+          const uint32_t h0 = pack4_fp8(y[0], y[1], y[2], y[3]), h1 = pack4_fp8(y[4], y[5], y[6], y[7]);
+          const v2f a0 = __builtin_amdgcn_cvt_pk_f32_fp8((int)h0, false), a1 = __builtin_amdgcn_cvt_pk_f32_fp8((int)h0, true);
+          const v2f a2 = __builtin_amdgcn_cvt_pk_f32_fp8((int)h1, false), a3 = __builtin_amdgcn_cvt_pk_f32_fp8((int)h1, true);
+          const uint32_t l0 = pack4_fp8((y[0] - a0[0]) * 16.f, (y[1] - a0[1]) * 16.f, (y[2] - a1[0]) * 16.f,
+                                        (y[3] - a1[1]) * 16.f);
+          const uint32_t l1 = pack4_fp8((y[4] - a2[0]) * 16.f, (y[5] - a2[1]) * 16.f, (y[6] - a3[0]) * 16.f,
+                                        (y[7] - a3[1]) * 16.f);
+          *reinterpret_cast<uint2*>(qst + 8 * i) = make_uint2(h0, h1);
+          *reinterpret_cast<uint2*>(qst + 16 * kQKDim + 8 * i) = make_uint2(l0, l1);
+        }
+      }
+      lds_barrier();
+      load_q(qst + l16 * kQKDim);
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) qlo[ks] = ld_v8(qst + 16 * kQKDim + l16 * kQKDim + 128 * ks + 32 * g);
+      qlo[4] = g < 2 ? ld_v8(qst + 16 * kQKDim + l16 * kQKDim + 512 + 32 * g) : v8i{0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+      for (int ks = 0; ks < 5; ++ks) asm volatile("" : "+v"(qlo[ks]));
+      c = __builtin_amdgcn_ldexpf(1.0f, (int)rmax[16 + l16]) * kvs * p.sm_scale * kLog2e;
+      lds_barrier();  // every wave holds its fragments (and its row exponent) before the stage is refilled
+    } else if constexpr (QB) {
       uint8_t* qst = smem + (C::S - 1) * C::STAGE;
       uint32_t* xu = reinterpret_cast<uint32_t*>(smem + C::OFF_X);
       const uint32_t m = (uint32_t)wave_max((int)qm);
@@ -401,7 +476,10 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
           for (int ks = 0; ks < 4; ++ks) ka[ks] = ld_v8(kp + 128 * ks + 32 * g);
           ka[4] = g < 2 ? ld_v8(kp + 512 + 32 * g) : v8i{0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
-          for (int ks = 0; ks < 5; ++ks) s = mfma16_f8(ka[ks], qv[ks], s);
+          for (int ks = 0; ks < 5; ++ks) {
+            s = mfma16_f8(ka[ks], qv[ks], s);
+            if constexpr (QM == 2) s = mfma16_f8_bscale(ka[ks], qlo[ks], 127 - 4, s);
+          }
         } else {
           const uint8_t* sp = sct + 4 * tok_of(w, l16);
           int ksc[5];
@@ -1029,10 +1107,16 @@ __global__ __launch_bounds__(256) void combine_kernel(const DecodeParams p) {
 template <bool IDX, bool QB>
 static hipError_t launch_decode_t(const DecodeParams& p, int kv_mode, int grid, hipStream_t stream) {
   if (p.num_heads == 16) {
+    if (QB && p.q_nparts == 0) {  // bf16 Q with no tensor-wide scale: a16w8, fp8 K only
+      if (kv_mode != 0) return hipErrorInvalidValue;
+      hipLaunchKernelGGL((decode_h16_kernel<0, 0, IDX, 2>), dim3(grid), dim3(256), 0, stream, p);
+      return hipGetLastError();
+    }
+    constexpr int QM = QB ? 1 : 0;
     switch (kv_mode) {
-      case 0: hipLaunchKernelGGL((decode_h16_kernel<0, 0, IDX, QB>), dim3(grid), dim3(256), 0, stream, p); break;
-      case 1: hipLaunchKernelGGL((decode_h16_kernel<1, 2, IDX, QB>), dim3(grid), dim3(256), 0, stream, p); break;
-      case 2: hipLaunchKernelGGL((decode_h16_kernel<1, 1, IDX, QB>), dim3(grid), dim3(256), 0, stream, p); break;
+      case 0: hipLaunchKernelGGL((decode_h16_kernel<0, 0, IDX, QM>), dim3(grid), dim3(256), 0, stream, p); break;
+      case 1: hipLaunchKernelGGL((decode_h16_kernel<1, 2, IDX, QM>), dim3(grid), dim3(256), 0, stream, p); break;
+      case 2: hipLaunchKernelGGL((decode_h16_kernel<1, 1, IDX, QM>), dim3(grid), dim3(256), 0, stream, p); break;
       default: return hipErrorInvalidValue;
     }
   } else if (p.num_heads == 128) {

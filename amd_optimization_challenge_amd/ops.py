@@ -262,7 +262,7 @@ def combine(batch: int, num_heads: int, ws: torch.Tensor, out: torch.Tensor, lse
 
 
 def decode_fwd(q, kv_data, kv_indptr, kv_indices, sm_scale, kv_mode="fp8", out=None, ws=None, q_seq_len=1,
-               return_lse=False, page_size=1, kv_last_page_lens=None):
+               return_lse=False, page_size=1, kv_last_page_lens=None, q_dtype="fp8"):
     """Whole operator: FP8-quantize q, plan, decode, combine.
 
     q: bf16 [rows, H, 576], rows = sequences x q_seq_len (row i of a sequence
@@ -271,6 +271,8 @@ def decode_fwd(q, kv_data, kv_indptr, kv_indices, sm_scale, kv_mode="fp8", out=N
     ``return_lse``.  page_size > 1: a paged cache as AITER's mla_decode_fwd
     takes it (caches [pages, page_size, 1, row], kv_indptr over pages,
     kv_indices = page ids, kv_last_page_lens), expanded on the device first.
+    q_dtype "bf16": the a16w8 route (``mla_decode_fwd_a16w8``; 16 heads, fp8
+    cache): Q keeps its own precision, no per-tensor quantization.
     """
     if int(page_size) != 1:
         if kv_indices is None or kv_last_page_lens is None:
@@ -294,11 +296,15 @@ def decode_fwd(q, kv_data, kv_indptr, kv_indices, sm_scale, kv_mode="fp8", out=N
     if out is None:
         out = torch.empty((batch, num_heads, V_DIM), dtype=torch.bfloat16, device=q.device)
     lse = torch.empty((batch, num_heads), dtype=torch.float32, device=q.device) if return_lse else None
+    if q_dtype not in ("fp8", "bf16"):
+        raise ValueError(f"q_dtype must be 'fp8' (a8w8: per-tensor Q quant) or 'bf16' (a16w8), got {q_dtype!r}")
+    fn, name = ((_lib.load().mla_decode_fwd, "mla_decode_fwd") if q_dtype == "fp8"
+                else (_lib.load().mla_decode_fwd_a16w8, "mla_decode_fwd_a16w8"))
     with torch.cuda.device(q.device):
-        _lib.check(_lib.load().mla_decode_fwd(
+        _lib.check(fn(
             _ptr(q), _ptr(k), ks, _ptr(ksc), kss, _ptr(v), vs, _ptr(sc), _ptr(kv_indptr),
             _ptr(kv_indices), batch, q_seq_len, num_heads, float(sm_scale), mode, _ptr(ws), ws.numel(),
-            _ptr(out), _ptr(lse), _stream()), "mla_decode_fwd")
+            _ptr(out), _ptr(lse), _stream()), name)
     return (out, lse) if return_lse else out
 
 

@@ -15,6 +15,8 @@ is taken to be ``arange * q_seq_len`` as generate_input makes it, :330), and
 a paged cache the way AITER's mla_decode_fwd does (aiter_mla.py:149-175): the
 caches shaped [pages, page_size, 1, row], ``kv_indptr`` over pages,
 ``config["kv_indices"]`` the page ids and ``config["kv_last_page_lens"]``.
+``config["q_dtype"] = "bf16"`` takes the reference's a16w8 route (bf16 Q, fp8
+cache, 16 heads; TASK/reference.py:55-58 Q_DTYPE) instead of a8w8.
 There is no fallback: a missing library or an unsupported shape raises.
 """
 from __future__ import annotations
@@ -45,4 +47,5 @@ def custom_kernel(data: input_t) -> output_t:
     page_size = int(config.get("page_size", 1))
     return ops.decode_fwd(q, kv_data, kv_indptr, kv_indices, sm_scale, kv_mode, q_seq_len=q_seq_len,
                           return_lse=bool(config.get("return_lse", False)), page_size=page_size,
-                          kv_last_page_lens=config.get("kv_last_page_lens"))
+                          kv_last_page_lens=config.get("kv_last_page_lens"),
+                          q_dtype=config.get("q_dtype", "fp8"))

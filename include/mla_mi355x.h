@@ -202,6 +202,23 @@ int mla_decode_fwd(const void* q_bf16, const void* k_cache, int64_t k_row_stride
                    int64_t workspace_bytes, void* out_bf16, float* lse_out, void* stream);
 
 /*
+ * The a16w8 route: bf16 Q against the fp8 cache with no tensor-wide Q scale,
+ * hence no amax pass -- the reference's bf16-Q paths (AITER's a16w8 decode,
+ * mixed-mla/submission.py:86-96 and :414-520 with q left in bf16).  Same
+ * arguments as mla_decode_fwd; 16 heads and kv_mode fp8 only
+ * (MLA_ERR_UNSUPPORTED otherwise).  Each head row of Q is split into two fp8
+ * terms at a power-of-two row scale inside the decode (about the 8
+ * significant bits of bf16), so scores are q . (k * kv_scale) * sm_scale with q
+ * as given rather than quantized per tensor.
+ */
+int mla_decode_fwd_a16w8(const void* q_bf16, const void* k_cache, int64_t k_row_stride,
+                         const void* k_scales, int64_t k_scale_stride, const void* v_cache,
+                         int64_t v_row_stride, const float* kv_scale, const int32_t* kv_indptr,
+                         const int32_t* kv_indices, int batch, int q_seq_len, int num_heads,
+                         float sm_scale, int kv_mode, void* workspace, int64_t workspace_bytes,
+                         void* out_bf16, float* lse_out, void* stream);
+
+/*
  * mla_decode_fwd without a caller workspace, for callers that cannot allocate
  * device memory (code under HIP graph capture, tight serving loops, harnesses
  * that forbid hipMalloc).  No counterpart in the reference.  Arguments mean what

@@ -451,15 +451,21 @@ def mla_decode_f64(q_deq, k_deq, v_deq, kv_indptr, kv_indices, sm_scale, q_seq_l
 
 
 def reference_path(q_bits, kv_mode, caches, kv_indptr, kv_indices, sm_scale, threads=None, q_seq_len=1,
-                   return_lse=False):
+                   return_lse=False, q_dtype="fp8"):
     """The full CPU restatement of the reference path for one decode call.
 
     quantize Q (a2) -> dequantize Q and KV -> fp32 attention -> bf16 bits.
+    q_dtype "bf16" is the a16w8 route (TASK/reference.py:55-58 Q_DTYPE, the
+    bf16-Q paths of mixed-mla/submission.py:414-520): Q enters as its bf16
+    values, unquantized.
     ``caches`` = dict(fp8_codes, fp8_scale, fp4_packed, fp4_scales) (numpy).
     Returns (out_bf16_bits [rows,H,512], out_f32[, lse [rows,H] natural log]).
     """
-    qc, qs = quantize_fp8_per_tensor(q_bits)
-    q_deq = dequant_fp8(qc, qs)
+    if q_dtype == "bf16":
+        q_deq = bf16_to_f32(np.asarray(q_bits, dtype=np.uint16))
+    else:
+        qc, qs = quantize_fp8_per_tensor(q_bits)
+        q_deq = dequant_fp8(qc, qs)
     k, v = dequant_kv(kv_mode, **caches)
     res = mla_decode(q_deq, k, v, kv_indptr, kv_indices, sm_scale, threads=threads, q_seq_len=q_seq_len,
                      return_lse=return_lse)

@@ -72,6 +72,13 @@ def test_argument_errors_without_device():
     assert lib.mla_expand_pages(16, 16, 16, 4, 64, 1 << 25, 16, 16, None) == _lib.MLA_ERR_INVALID_ARGUMENT
     assert b"2^31" in lib.mla_last_error()
     assert lib.mla_expand_pages(None, None, None, 4, 8, 10, None, None, None) == _lib.MLA_ERR_INVALID_ARGUMENT
+    # the a16w8 route: 16 heads and the fp8 cache only
+    assert lib.mla_decode_fwd_a16w8(None, None, 576, None, 0, None, 0, None, None, None, 4, 1, 128, 0.1, 0,
+                                    None, 0, None, None, None) == _lib.MLA_ERR_UNSUPPORTED
+    assert lib.mla_decode_fwd_a16w8(None, None, 288, None, 18, None, 0, None, None, None, 4, 1, 16, 0.1, 1,
+                                    None, 0, None, None, None) == _lib.MLA_ERR_UNSUPPORTED
+    assert lib.mla_decode_fwd_a16w8(None, None, 576, None, 0, None, 0, None, None, None, 4, 1, 16, 0.1, 0,
+                                    None, 0, None, None, None) == _lib.MLA_ERR_INVALID_ARGUMENT
     # the no-alloc variant: stated scratch size, shape errors before any device call
     assert lib.mla_noalloc_scratch_bytes() == 64 << 20
     assert lib.mla_decode_fwd_noalloc(None, None, 576, None, 0, None, 0, None, None, None, 4, 1, 24, 0.1, 0,
