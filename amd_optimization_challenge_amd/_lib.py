@@ -17,7 +17,7 @@ MLA_ERR_UNSUPPORTED = 2
 MLA_ERR_WORKSPACE_TOO_SMALL = 3
 MLA_ERR_HIP = 4
 
-KV_MODES = {"fp8": 0, "mxfp4": 1, "mxfp4k_fp8v": 2}
+KV_MODES = {"fp8": 0, "mxfp4": 1, "mxfp4k_fp8v": 2, "bf16": 3}
 
 # Every entry point the header declares, with its ctypes signature.
 _P = ctypes.c_void_p

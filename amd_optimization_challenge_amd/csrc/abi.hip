@@ -66,10 +66,12 @@ int check_shape(int batch, int num_heads, int kv_mode) {
   if (batch < 1) return set_error(MLA_ERR_INVALID_ARGUMENT, "batch must be >= 1 (got %d)", batch);
   if (num_heads != 16 && num_heads != 128)
     return set_error(MLA_ERR_UNSUPPORTED, "num_heads must be 16 or 128 (got %d)", num_heads);
-  if (kv_mode < MLA_KV_FP8 || kv_mode > MLA_KV_MXFP4K_FP8V)
+  if (kv_mode < MLA_KV_FP8 || kv_mode > MLA_KV_BF16)
     return set_error(MLA_ERR_INVALID_ARGUMENT, "unknown kv_mode %d", kv_mode);
   if (num_heads == 128 && kv_mode == MLA_KV_MXFP4)
     return set_error(MLA_ERR_UNSUPPORTED, "kv_mode mxfp4 (fp4 V) is implemented for num_heads=16 only");
+  if (num_heads == 128 && kv_mode == MLA_KV_BF16)
+    return set_error(MLA_ERR_UNSUPPORTED, "kv_mode bf16 (a16w16) is implemented for num_heads=16 only");
   return MLA_OK;
 }
 
@@ -137,8 +139,8 @@ int decode_params(const void* q_fp8, const float* q_scale, const void* k_cache, 
   if (!aligned(q_fp8, 16) || !aligned(k_cache, 16) || !aligned(out, 16))
     return set_error(MLA_ERR_INVALID_ARGUMENT, "q, k_cache and out must be 16-byte aligned");
   if (!(sm_scale > 0.f)) return set_error(MLA_ERR_INVALID_ARGUMENT, "sm_scale must be > 0");
-  const bool k_fp4 = kv_mode != MLA_KV_FP8;
-  const int64_t krow = k_fp4 ? kFp4RowBytes : kQKDim;
+  const bool k_fp4 = kv_mode == MLA_KV_MXFP4 || kv_mode == MLA_KV_MXFP4K_FP8V;
+  const int64_t krow = kv_mode == MLA_KV_BF16 ? 2 * kQKDim : (k_fp4 ? kFp4RowBytes : kQKDim);
   if (k_row_stride < krow || (k_row_stride % 16) != 0)
     return set_error(MLA_ERR_INVALID_ARGUMENT, "k_row_stride must be >= %lld and a multiple of 16 (got %lld)",
                 (long long)krow, (long long)k_row_stride);
@@ -152,7 +154,8 @@ int decode_params(const void* q_fp8, const float* q_scale, const void* k_cache, 
     if (v_row_stride < kVDim || (v_row_stride % 16) != 0)
       return set_error(MLA_ERR_INVALID_ARGUMENT, "v_row_stride must be >= 512 and a multiple of 16");
   }
-  if (kv_mode != MLA_KV_MXFP4 && !kv_scale) return set_error(MLA_ERR_INVALID_ARGUMENT, "fp8 cache needs kv_scale");
+  if ((kv_mode == MLA_KV_FP8 || kv_mode == MLA_KV_MXFP4K_FP8V) && !kv_scale)
+    return set_error(MLA_ERR_INVALID_ARGUMENT, "fp8 cache needs kv_scale");
   char* ws = static_cast<char*>(workspace);
   p->q_fp8 = static_cast<const uint8_t*>(q_fp8);
   p->q_scale = q_scale;
@@ -324,6 +327,8 @@ int mla_decode(const void* q_fp8, const float* q_scale, const void* k_cache, int
                const float* kv_scale, const int32_t* kv_indptr, const int32_t* kv_indices, int batch,
                int num_heads, float sm_scale, int kv_mode, void* workspace, int64_t workspace_bytes,
                void* out_bf16, float* lse_out, void* stream) {
+  if (kv_mode == MLA_KV_BF16)
+    return set_error(MLA_ERR_UNSUPPORTED, "the bf16 cache takes bf16 Q: use mla_decode_fwd (kv_mode bf16)");
   DecodeParams p;
   WsLayout L;
   int rc = decode_params(q_fp8, q_scale, k_cache, k_row_stride, k_scales, k_scale_stride, v_cache,
@@ -390,6 +395,17 @@ int mla_decode_fwd(const void* q_bf16, const void* k_cache, int64_t k_row_stride
   const int64_t n = (int64_t)batch * num_heads * kQKDim;
   uint32_t* partials = reinterpret_cast<uint32_t*>(ws + L.quant_off);
   int nb = 0;
+  if (kv_mode == MLA_KV_BF16) {  // a16w16: Q is used as it is, no amax pass
+    hipError_t e = launch_plan(kv_indptr, batch, q_seq_len, target_items_for(batch, num_heads, kv_mode, ncu),
+                               L.max_items, reinterpret_cast<int32_t*>(ws + L.plan_off), s);
+    if (e != hipSuccess) return hip_fail(e, "plan launch");
+    p.q_bf16 = static_cast<const uint16_t*>(q_bf16);
+    e = launch_decode(p, kv_mode, L.max_items, s);
+    if (e != hipSuccess) return hip_fail(e, "decode launch");
+    e = launch_combine(p, s);
+    if (e != hipSuccess) return hip_fail(e, "combine launch");
+    return MLA_OK;
+  }
   hipError_t e = launch_amax(static_cast<const uint16_t*>(q_bf16), n, partials, &nb, kv_indptr,
                              static_cast<const int32_t*>(kv_indices), batch, q_seq_len,
                              target_items_for(batch, num_heads, kv_mode, ncu),

@@ -112,12 +112,15 @@ __device__ __forceinline__ void wait_groups(int k) {
 // than kVScaleSpan above E_ref, restarts the item from a higher reference
 // (block-wide vote), so neither the accumulators nor P' can overflow.
 // ============================================================================
+// KF / VF: 0 / 0 fp8 K = V, 1 / 2 fp4 K = V, 1 / 1 fp4 K + fp8 V, 2 / 3 bf16 K =
+// V (a16w16: 1152-byte rows, V = their first 512 dims; QK and PV on 16x16x32
+// bf16 MFMAs, the V^T operand by ds_read_b64_tr_b16).
 template <int KF, int VF>
 struct H16 {
-  static constexpr int KROW = KF == 0 ? 576 : 288;
-  static constexpr int KST = KROW + 16;                        // LDS row stride: 592 / 304
-  static constexpr int KCPR = KST / 16;                        // 16-B chunks per LDS row: 37 / 19
-  static constexpr int KCH = KROW / 16;                        // real chunks: 36 / 18
+  static constexpr int KROW = KF == 0 ? 576 : (KF == 1 ? 288 : 1152);
+  static constexpr int KST = KROW + 16;                        // LDS row stride: 592 / 304 / 1168
+  static constexpr int KCPR = KST / 16;                        // 16-B chunks per LDS row: 37 / 19 / 73
+  static constexpr int KCH = KROW / 16;                        // real chunks: 36 / 18 / 72
   static constexpr int VST = 528, VCPR = 33;                   // fp8 V rows (VF == 1): 512 B used
   static constexpr int KW = kTile * KST / 1024;                // 1-KiB DMA windows of K rows: 37 / 19
   static constexpr int VW = VF == 1 ? kTile * VST / 1024 : 0;  // of V rows: 33
@@ -128,8 +131,8 @@ struct H16 {
   // registers a wave), whose eight waves keep twice the row gathers in flight
   // and overlap one group's compute with the other's waits.  fp4 K + fp8 V
   // (two caches) runs one work-group per CU.
-  static constexpr int S = KF == 0 ? 2 : (VF == 1 ? 2 : 3);
-  static constexpr int BLOCKS_PER_CU = VF == 1 ? 1 : 2;
+  static constexpr int S = KF != 1 ? 2 : (VF == 1 ? 2 : 3);
+  static constexpr int BLOCKS_PER_CU = (VF == 1 || KF == 2) ? 1 : 2;
   // DMA issue: waves RW0..3 gather rows.  fp4 K + fp8 V: wave 0 gathers the
   // 18 scale bytes of every token (SCW = 1); fp4 K = V: every wave gathers rows
   // and scale byte columns j = w + 4k (SCW = 4), so no wave issues a long burst
@@ -139,13 +142,14 @@ struct H16 {
   static constexpr int NA = (NW + NRW - 1) / NRW;              // windows per row wave: NA or NA - 1
   static constexpr int NAW = NW % NRW == 0 ? NRW : NW % NRW;   // row waves (from RW0) that issue NA
   static constexpr bool VB16 = VF == 2;                        // fp4 V, bf16 PV from registers
-  static constexpr int PST = 68;                               // f32 P row stride (VB16): 64 tokens + 4
+  static constexpr bool P32 = VF >= 2;                         // P shared as f32 [head][token] (bf16 PV)
+  static constexpr int PST = 68;                               // f32 P row stride (P32): 64 tokens + 4
   static constexpr int NSL = 2 * S;                            // slot stages (slots lead rows by S tiles)
   static constexpr int OFF_SLOT = S * STAGE;                   // [NSL][64] int32 cache slots
   static constexpr int SCST = kMxBlocks * 256;                 // e8m0 stage: [18 blocks][64 tokens] dwords
   static constexpr int OFF_SC = OFF_SLOT + NSL * 256;          // [S] e8m0 stages (KF == 1)
   static constexpr int OFF_P = OFF_SC + (KF == 1 ? S * SCST : 0);
-  static constexpr int P_BYTES = VB16 ? 16 * PST * 4 : 2 * 4 * 16 * 16;  // f32 [h][token] | fp8 [term][g][h][16]
+  static constexpr int P_BYTES = P32 ? 16 * PST * 4 : 2 * 4 * 16 * 16;  // f32 [h][token] | fp8 [term][g][h][16]
   static constexpr int OFF_PS = OFF_P + P_BYTES;               // [g][h] e8m0 B scales
   static constexpr int OFF_X = OFF_PS + 64;                    // [4][16] f32 exchange
   static constexpr int OFF_E = OFF_X + 256;                    // [4] int exchange (V block exponents)
@@ -162,11 +166,13 @@ constexpr int kVScaleSpan = 31;  // fp4 V: P' = P 2^(e - E_ref) <= 2^(96 + 31) s
 // split here into two fp8 terms at a power-of-two row scale 2^e, hi =
 // e4m3(q 2^-e) and lo = e4m3((q 2^-e - hi) 2^4), and QK runs one MFMA per term
 // (the lo one with B scale 2^-4), about 8 significant bits of Q as bf16 has.
+// 3: bf16, used as it is (a16w16, bf16 K).
 template <int KF, int VF, bool IDX, int QM>
 __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_kernel(const DecodeParams p) {
   using C = H16<KF, VF>;
   constexpr bool QB = QM != 0;
   static_assert(QM != 2 || KF == 0, "a16w8: fp8 K only");
+  static_assert((QM == 3) == (KF == 2), "a16w16: bf16 Q with bf16 K");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[C::LDS];
   const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
 
@@ -283,6 +289,7 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
   // gathered in that order.  With fp8 K both operands share one order.
   v8i qv[5];
   v8i qlo[QM == 2 ? 5 : 1];  // a16w8: the lo term of Q
+  v8bf qbf[QM == 3 ? 18 : 1];  // a16w16: Q^T bf16, K-step ks = dims 32ks + 8g .. +7
   float c = 0.f;  // qs * kv scale (fp8 K) * sm_scale * log2(e), set once Q is resident
   const float kvs = (KF == 0 || VF == 1) ? p.kv_scale[0] : 1.0f;
   const float vscale = VF == 2 ? 1.0f : kvs;
@@ -318,12 +325,21 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
     for (int k = w; k < QNV / 64; k += 4) dma16_to_lds(src + 1024 * k + 16 * lane, qlds + 1024 * k);
     if constexpr (QM == 1)
       for (int i = tid; i < p.q_nparts; i += 256) qm = max(qm, p.q_partials[i]);
+    (void)qm;
   } else {
     load_q(p.q_fp8 + ((int64_t)b * 16 + l16) * kQKDim);
     c = p.q_scale[0] * (KF == 0 ? kvs : 1.0f) * p.sm_scale * kLog2e;
   }
   auto quantize_q = [&]() __attribute__((always_inline)) {  // block-uniform; the loads have landed
-    if constexpr (QM == 2) {
+    if constexpr (QM == 3) {
+      const uint8_t* qrow = smem + (C::S - 1) * C::STAGE + l16 * (2 * kQKDim) + 16 * g;
+#pragma unroll
+      for (int ks = 0; ks < 18; ++ks) qbf[ks] = __builtin_bit_cast(v8bf, *reinterpret_cast<const uint4*>(qrow + 64 * ks));
+#pragma unroll
+      for (int ks = 0; ks < 18; ++ks) asm volatile("" : "+v"(qbf[ks]));  // keep resident, no reload
+      c = p.sm_scale * kLog2e;
+      lds_barrier();  // every wave holds its fragments before the stage is refilled
+    } else if constexpr (QM == 2) {
       // per head row: |q| max (bf16 bits) -> row exponent e (q 2^-e <= 448),
       // then both terms written over the bf16 rows (hi at row r, lo 9 KiB on)
       uint8_t* qst = smem + (C::S - 1) * C::STAGE;
@@ -471,7 +487,15 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
         // all fragment reads first, then the MFMA chain
         const uint8_t* kp = kt + tok_of(w, l16) * C::KST;
         v8i ka[5];
-        if constexpr (KF == 0) {
+        if constexpr (KF == 2) {
+          // 18 steps of 32 dims, reads two steps ahead of their MFMA
+          v8bf kb[18];
+#pragma unroll
+          for (int ks = 0; ks < 18; ++ks) kb[ks] = __builtin_bit_cast(v8bf, *reinterpret_cast<const uint4*>(kp + 64 * ks + 16 * g));
+#pragma unroll
+          for (int ks = 0; ks < 18; ++ks) s = mfma16x32_bf16(kb[ks], qbf[ks], s);
+          (void)ka;
+        } else if constexpr (KF == 0) {
 #pragma unroll
           for (int ks = 0; ks < 4; ++ks) ka[ks] = ld_v8(kp + 128 * ks + 32 * g);
           ka[4] = g < 2 ? ld_v8(kp + 512 + 32 * g) : v8i{0, 0, 0, 0, 0, 0, 0, 0};
@@ -521,7 +545,7 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
       const bool over = __any(m_w > m_ref + kRebase) || (C::VB16 && e_w > e_ref + kVScaleSpan);
       if (lane == 0) vote[w] = over ? 1 : 0;
 
-      if constexpr (!C::VB16) {
+      if constexpr (!C::P32) {
         // P' = 2^(s - m_w) * 2^8 (two fp8 terms); B scale 2^(m_w - m_ref - 8)
         const float mw = m_w == neg_inf() ? m_ref : m_w;
         const float dm = fminf(fmaxf(mw - m_ref, -160.f), 160.f);
@@ -556,7 +580,35 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
       }
 
       // ---- O^T[dims 128w ..] += V^T . P^T ---------------------------------------
-      if constexpr (!C::VB16) {
+      if constexpr (VF == 3) {
+        // bf16 V: two 32-token K steps of 16x16x32 bf16 MFMAs per 16-dim tile;
+        // lane (m, g) holds tokens 32h + 8g .. +7 of step h in both operands.
+        // V^T by ds_read_b64_tr_b16: within a 16-lane group, result lane j,
+        // element i = element j & 3 of source lane 4i + (j >> 2); source lane
+        // s reads token 8g + 4u + (s >> 2), dims 16dt + 4(s & 3) .. +3, so read
+        // u gives lane m tokens 8g + 4u .. +3 of dim 16dt + m.
+        const float* prow = reinterpret_cast<const float*>(smem + C::OFF_P) + l16 * C::PST;
+        v8bf pb[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const float4 pa = *reinterpret_cast<const float4*>(prow + 32 * h + 8 * g);
+          const float4 pc = *reinterpret_cast<const float4*>(prow + 32 * h + 8 * g + 4);
+          pb[h] = __builtin_bit_cast(v8bf, make_uint4(pack_bf16x2(pa.x, pa.y), pack_bf16x2(pa.z, pa.w),
+                                                      pack_bf16x2(pc.x, pc.y), pack_bf16x2(pc.z, pc.w)));
+        }
+        const uint32_t vb = lds0 + st * C::STAGE + (8 * g + (l16 >> 2)) * C::KST + 2 * (128 * w + 4 * (l16 & 3));
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const uint32_t a = vb + (32 * h) * C::KST + 32 * dt;
+            const v4s16 r0 = lds_read_tr16(a);
+            const v4s16 r1 = lds_read_tr16(a + 4 * C::KST);
+            const v8bf av = __builtin_bit_cast(v8bf, v8s16{r0[0], r0[1], r0[2], r0[3], r1[0], r1[1], r1[2], r1[3]});
+            o[dt] = mfma16x32_bf16(av, pb[h], o[dt]);
+          }
+        }
+      } else if constexpr (!C::VB16) {
         // The block-scaled MFMA takes fp8 byte j of lane group G as K index
         // 16G + (j & 15) + 64 (j >> 4), scaled by lane group K/32.  Wave gw's
         // 16 tokens therefore sit in K block gw: bytes 0-7 of group G hold
@@ -1107,6 +1159,11 @@ __global__ __launch_bounds__(256) void combine_kernel(const DecodeParams p) {
 template <bool IDX, bool QB>
 static hipError_t launch_decode_t(const DecodeParams& p, int kv_mode, int grid, hipStream_t stream) {
   if (p.num_heads == 16) {
+    if (kv_mode == 3) {  // bf16 cache: bf16 Q, used as it is
+      if (!QB) return hipErrorInvalidValue;
+      hipLaunchKernelGGL((decode_h16_kernel<2, 3, IDX, 3>), dim3(grid), dim3(256), 0, stream, p);
+      return hipGetLastError();
+    }
     if (QB && p.q_nparts == 0) {  // bf16 Q with no tensor-wide scale: a16w8, fp8 K only
       if (kv_mode != 0) return hipErrorInvalidValue;
       hipLaunchKernelGGL((decode_h16_kernel<0, 0, IDX, 2>), dim3(grid), dim3(256), 0, stream, p);

@@ -266,6 +266,15 @@ __device__ __forceinline__ v2i lds_read_tr8(uint32_t lds_off) {
   typedef __attribute__((address_space(3))) v2i lds_v2i;
   return __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(uintptr_t)lds_off);
 }
+// ds_read_b64_tr_b16: within each 16-lane group, result lane j gets element
+// (j & 3) of the four 16-bit elements read by lane 4i + (j >> 2) as its element
+// i, i = 0..3 (a 16 x 4 -> 4 x 16 element transpose).
+typedef short v4s16 __attribute__((ext_vector_type(4)));
+typedef short v8s16 __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ v4s16 lds_read_tr16(uint32_t lds_off) {
+  typedef __attribute__((address_space(3))) v4s16 lds_v4s16;
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s16*)(uintptr_t)lds_off);
+}
 // ds_read_b64_tr_b4: within each 16-lane group, result lane j gets nibble j of
 // the 8-byte read of lane m as its nibble m, m = 0..15 (a 16 x 16 nibble
 // transpose)

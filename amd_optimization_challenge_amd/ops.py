@@ -186,7 +186,7 @@ def append_kv(x: torch.Tensor, slots: torch.Tensor | None, fp8=None, mxfp4=None,
 def _rows(x: torch.Tensor) -> torch.Tensor:
     """The cache as [rows, bytes per row]: every leading dimension (tokens, or
     pages x page_size x kv heads of a paged cache) flattened into rows."""
-    x = as_bytes(x)
+    x = x.view(torch.uint8) if x.dtype == torch.bfloat16 else as_bytes(x)
     return x if x.dim() == 2 else x.flatten(0, x.dim() - 2)
 
 
@@ -208,6 +208,11 @@ def _kv_args(kv_mode: int, kv_data: dict):
         s = _rows(e8)
         v = _rows(fp8)
         return k, k.stride(0), s, s.stride(0), v, v.stride(0), sc
+    if kv_mode == 3:
+        k = _rows(kv_data["bf16"])
+        if kv_data["bf16"].dtype != torch.bfloat16:
+            raise ValueError("kv_data['bf16'] must be a bf16 tensor")
+        return k, k.stride(0), None, 0, None, 0, None
     raise ValueError(kv_mode)
 
 

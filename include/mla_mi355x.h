@@ -49,6 +49,8 @@ extern "C" {
 #define MLA_KV_FP8 0          /* K = V = fp8 cache (V = first 512 dims)            */
 #define MLA_KV_MXFP4 1        /* K = V = mxfp4 cache (V = first 256 B + 16 scales)   */
 #define MLA_KV_MXFP4K_FP8V 2  /* K = mxfp4 cache, V = first 512 dims of fp8 cache    */
+#define MLA_KV_BF16 3         /* K = V = bf16 cache (a16w16; V = first 512 dims),     */
+                              /* 16 heads, mla_decode_fwd only (Q used as given)      */
 
 /* Message describing the last failure on this thread ("" if none). */
 const char* mla_last_error(void);

@@ -319,13 +319,18 @@ def dequant_mxfp4(packed: np.ndarray, scales: np.ndarray, cols: int) -> np.ndarr
 
 
 def dequant_kv(kv_mode: str, fp8_codes=None, fp8_scale=None, fp4_packed=None,
-               fp4_scales=None) -> tuple[np.ndarray, np.ndarray]:
+               fp4_scales=None, bf16_bits=None) -> tuple[np.ndarray, np.ndarray]:
     """Return (K [T,576] f32, V [T,512] f32) for a kv_mode.
 
     fp8          : K = V-source = fp8 cache (V = first 512 dims)
     mxfp4        : K = mxfp4 cache, V = first 512 dims of the same cache
     mxfp4k_fp8v  : K = mxfp4 cache (576), V = fp8 cache (first 512 dims)
+    bf16         : K = the bf16 cache as it is (TASK/reference.py:55-58
+                   KV_DTYPE = bf16, kv_data["bf16"] of :311-327), V = first 512
     """
+    if kv_mode == "bf16":
+        k = bf16_to_f32(np.asarray(bf16_bits, dtype=np.uint16).reshape(-1, QK_DIM))
+        return k, k[:, :V_DIM]
     if kv_mode == "fp8":
         k = dequant_fp8(fp8_codes.reshape(-1, QK_DIM), fp8_scale)
         return k, k[:, :V_DIM]

@@ -37,6 +37,11 @@ def test_argument_errors_without_device():
     assert lib.mla_workspace_bytes(0, 16, 0, ctypes.byref(n)) == _lib.MLA_ERR_INVALID_ARGUMENT
     assert lib.mla_workspace_bytes(4, 128, 1, ctypes.byref(n)) == _lib.MLA_ERR_UNSUPPORTED
     assert lib.mla_workspace_bytes(4, 16, 7, ctypes.byref(n)) == _lib.MLA_ERR_INVALID_ARGUMENT
+    # the bf16 cache (a16w16): 16 heads, bf16 Q through mla_decode_fwd only
+    assert lib.mla_workspace_bytes(4, 16, 3, ctypes.byref(n)) == _lib.MLA_OK
+    assert lib.mla_workspace_bytes(4, 128, 3, ctypes.byref(n)) == _lib.MLA_ERR_UNSUPPORTED
+    assert lib.mla_decode(None, None, None, 1152, None, 0, None, 0, None, None, None, 4, 16, 0.1, 3, None, 0,
+                          None, None, None) == _lib.MLA_ERR_UNSUPPORTED
     assert lib.mla_pack_mxfp4(None, 4, 33, 66, None, 16, None, 2, None) == _lib.MLA_ERR_INVALID_ARGUMENT
     assert lib.mla_quant_fp8_per_tensor(None, 0, None, None, None, 0, None) == _lib.MLA_ERR_INVALID_ARGUMENT
     assert lib.mla_selftest(0, None, None, None) == _lib.MLA_ERR_INVALID_ARGUMENT
