@@ -1,23 +1,21 @@
-// Split-KV MLA absorbed decode for gfx950 and the log-sum-exp split combine.
+// Split-KV MLA absorbed decode for gfx950 with 16 heads, the launch switch for
+// every head count and cache mode, and the log-sum-exp split combine.
 //
 // One work-group (4 waves) runs one work item {batch, token range, slot} from
-// the on-device plan.  Per 64-token tile the group gathers the cache rows named
-// by kv_indices (page size 1) from HBM with 16-byte loads into registers one
-// tile ahead, then writes them to LDS twice: row-major (the QK operand, one
-// token per MFMA row) and transposed (the PV operand, one latent dim per MFMA
-// row).  Both products run on MFMA:
+// the on-device plan.  Cache rows are gathered by kv_indices (page tables are
+// expanded to that form beforehand) straight from HBM into an LDS ring by
+// LDS-DMA, slot indices one tile ahead of the rows they address.  Both
+// products run on MFMA:
 //   scores  S^T = K . Q^T   K = A operand from LDS, Q = B operand in registers
-//   output  O^T = V^T . P^T V^T = A operand from LDS, P = B operand
-// so every lane's accumulators belong to a single head and the online-softmax
-// rescale is a per-lane scalar.  Heads: H = 16 runs the four waves on four
-// 16-token slices of the tile and splits the 512 output dims four ways (the
-// tile max and P go through LDS); H = 128 gives each wave 32 heads of its own
-// (32x32x64 MFMAs, softmax wave-local, P stays in registers).
+//   output  O^T = V^T . P^T V^T = A operand from LDS (transpose reads), P = B
+// so every lane's accumulators belong to a single head and the softmax state
+// is a per-lane scalar.  H = 16 runs here (below); H = 128 gives each wave 32
+// heads of its own (decode_h128.hip).
 //
-// Numerics: scores are accumulated in f32 from the fp8/fp4 operands and scaled
-// by q_scale * k_scale * sm_scale * log2(e); the softmax uses exp2.  P enters
-// the PV product as fp8 e4m3 (x256 to stay clear of the subnormal range) or as
-// bf16 when V comes from the MXFP4 cache.  The row sum uses the f32 P.
+// Numerics: scores are accumulated in f32 from the fp8/fp4/bf16 operands and
+// scaled by q_scale * k_scale * sm_scale * log2(e); the softmax uses exp2 with
+// a fixed per-item reference.  P enters the PV product as two fp8 terms (fp8
+// V), or as bf16 (fp4 or bf16 V).  The row sum uses the f32 P.
 //
 // Behavioural reference: mixed-mla/asm_dumps/aiter_mla.py:149-470 (interface),
 // mixed-mla/submission.py:122-250 (split-K online softmax), V5
@@ -31,7 +29,7 @@ namespace mla {
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kPScale = 256.0f;  // fp8 P = p * 256
-constexpr float kRebase = 96.0f;   // H128: max log2 distance of a tile max above the fixed reference
+constexpr float kRebase = 96.0f;   // max log2 distance of a tile max above the fixed reference
 
 __device__ __forceinline__ v8i ld_v8(const uint8_t* p) {
   uint4 a = *reinterpret_cast<const uint4*>(p);
@@ -751,351 +749,6 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
 }
 
 // ============================================================================
-// Q^T B-operand fragments of one lane of the H = 128 kernels: for K-step ks,
-// the 16 fp8 bytes at dims o = 64 ks + S0 hh and the 16 at o + D1 of the
-// lane's head row, kept resident in registers.
-// ============================================================================
-template <int S0, int D1>
-__device__ __forceinline__ void load_q128(const DecodeParams& p, int b, int head, int hh, v8i (&qv)[9]) {
-  const uint8_t* qrow = p.q_fp8 + ((int64_t)b * 128 + head) * kQKDim;
-#pragma unroll
-  for (int ks = 0; ks < 9; ++ks) {
-    const int o = 64 * ks + S0 * hh;
-    const uint4 lo = *reinterpret_cast<const uint4*>(qrow + o);
-    const uint4 hi = *reinterpret_cast<const uint4*>(qrow + o + D1);
-    qv[ks] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-  }
-#pragma unroll
-  for (int ks = 0; ks < 9; ++ks) asm volatile("" : "+v"(qv[ks]));  // keep resident, no reload
-}
-
-// ============================================================================
-// H = 128.  4 waves; wave w owns heads 32w .. 32w+31 for every token of the
-// work item and all 512 latent dims, so the softmax state and O^T never leave
-// the wave.  Q^T (the QK B operand) stays in registers, O^T in accumulators.
-// Cache rows are gathered straight into an LDS ring by LDS-DMA (no staging
-// registers), two tiles deep; the PV A operand (V^T) is read from the row-major
-// tile with ds_read_b64_tr_b8, so no transposed copy is ever written.  This
-// kernel serves the two-cache mode: fp4 K rows + e8m0 scales for QK, the fp8
-// cache's rows for V (the fp8-only mode runs decode_h128f_kernel, decode_h128.hip).
-// Online softmax is rescaled lazily: the exponent base m only moves when a
-// head's tile max exceeds it by more than 8 (log2 units), so P <= 2^8 fits
-// e4m3 and O^T is touched by VALU only on those (rare) tiles.
-// ============================================================================
-struct H128 {
-  static constexpr int NT = 256;
-  static constexpr int KST = 304;                              // fp4 K row stride in LDS
-  static constexpr int KCH = 18;                               // real 16-B chunks per K row
-  static constexpr int VST = 528;                              // fp8 V row stride
-  static constexpr int KDMA = (kTile * KST + 1023) / 1024;     // 1-KiB DMA windows: 19
-  static constexpr int VDMA = (kTile * VST + 1023) / 1024;     // 33
-  static constexpr int DPW = (KDMA + VDMA + 3) / 4;            // windows per wave: 13
-  static constexpr int STAGE = 4 * DPW * 1024;                 // ring stage bytes
-  static constexpr int S = 2;                                  // ring depth (tiles)
-  static constexpr int OFF_V = KDMA * 1024;                    // V rows inside a stage
-  static constexpr int OFF_SLOT = S * STAGE;                   // [S][64] int32 cache slots
-  static constexpr int OFF_VOTE = OFF_SLOT + S * 256;          // [2][4] restart votes
-  static constexpr int LDS = OFF_VOTE + 16;
-};
-
-template <bool IDX>
-__global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams p) {
-  using C = H128;
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[C::LDS];
-  const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
-
-  const int32_t* plan = p.plan;
-  if ((int)blockIdx.x >= plan[0]) return;
-  const int4 it = reinterpret_cast<const int4*>(plan + kPlanHeader)[blockIdx.x];
-  const int b = it.x, t_beg = it.y, t_end = it.z, slot = it.w;
-  const int ntok = t_end - t_beg;
-  const int ntiles = (ntok + kTile - 1) / kTile;
-
-  const int tid = threadIdx.x;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (feeds M0)
-  const int lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
-  const int head = 32 * w + l32;
-
-  // ---- Q^T B operand, K-step ks = dims 64ks .. +63 (fp4 K partner order) -----
-  v8i qv[9];
-  load_q128<16, 32>(p, b, head, hh, qv);
-  const float qs = p.q_scale[0];
-  const float kvs = p.kv_scale[0];
-  const float c = qs * p.sm_scale * kLog2e;  // K's scales ride on the MFMA's A scale
-  const float vscale = kvs;  // the 2^8 carried by P' is folded into the PV scale exponent
-
-  v16f o[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) o[i] = v16f{};
-  float m_ref = 0.f, l_run = 0.f;
-
-  // ---- DMA issue helpers -------------------------------------------------------
-  auto slot_of = [&](int st, int tok, int pos0) -> int {
-    if constexpr (IDX) return reinterpret_cast<const int*>(smem + C::OFF_SLOT + st * 256)[tok];
-    else return min(pos0 + tok, t_end - 1);
-  };
-  auto issue_slots = [&](int t) {  // wave 0: 64 slots of tile t (positions clamped into the item)
-    if constexpr (IDX) {
-      if (w == 0) {
-        const int pos = min(t_beg + kTile * t + lane, t_end - 1);
-        dma4_to_lds(p.kv_indices + pos, lds0 + C::OFF_SLOT + (t % C::S) * 256);
-      }
-    }
-  };
-  auto issue_rows = [&](int t) {  // this wave's DPW windows of tile t
-    const int st = t % C::S;
-    const int pos0 = t_beg + kTile * t;
-    const uint32_t sbase = lds0 + st * C::STAGE;
-    // all slot reads first: each DMA below is an asm barrier for memory ops
-    int sl[C::DPW], co[C::DPW];
-#pragma unroll
-    for (int k = 0; k < C::DPW; ++k) {
-      const int u = w + 4 * k;  // window index within the stage
-      if (u < C::KDMA) {
-        const int bb = 1024 * u + 16 * lane;
-        int tok = bb / C::KST, pos = (bb - tok * C::KST) >> 4;
-        if (tok >= kTile) { tok = kTile - 1; pos = 0; }
-        sl[k] = slot_of(st, tok, pos0);
-        co[k] = 16 * min(pos, C::KCH - 1);
-      } else if (u < C::KDMA + C::VDMA) {
-        const int bb = 1024 * (u - C::KDMA) + 16 * lane;
-        int tok = bb / C::VST, pos = (bb - tok * C::VST) >> 4;
-        if (tok >= kTile) { tok = kTile - 1; pos = 0; }
-        sl[k] = slot_of(st, tok, pos0);
-        co[k] = 16 * min(pos, 31);
-      } else {  // padding window: any valid source
-        sl[k] = slot_of(st, kTile - 1, pos0);
-        co[k] = 0;
-      }
-    }
-#pragma unroll
-    for (int k = 0; k < C::DPW; ++k) {
-      const int u = w + 4 * k;
-      const bool vrow = u >= C::KDMA && u < C::KDMA + C::VDMA;
-      const uint8_t* src = vrow ? p.v_cache + (int64_t)sl[k] * p.v_row_stride + co[k]
-                                : p.k_cache + (int64_t)sl[k] * p.k_row_stride + co[k];
-      dma16_to_lds(src, sbase + 1024 * u);
-    }
-  };
-  // fp4 K scales: lane (token u*32 + l32) needs blocks 2ks + hh, ks = 0..8
-  uint32_t sc_nxt[2][9], sc_cur[2][9];
-  auto load_scales = [&](int t) {
-    const int st = t % C::S;
-    const int pos0 = t_beg + kTile * t;
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const uint8_t* srow = p.k_scales + (int64_t)slot_of(st, 32 * u + l32, pos0) * p.k_scale_stride;
-#pragma unroll
-      for (int ks = 0; ks < 9; ++ks) sc_nxt[u][ks] = srow[2 * ks + hh];
-    }
-  };
-
-  auto prologue = [&]() {
-    // slots(0) visible; then rows(0) + scales(0) and slots(1) in flight
-    issue_slots(0);
-    wait_vmcnt<0>();
-    lds_barrier();
-    issue_slots(1);
-    issue_rows(0);
-    load_scales(0);
-  };
-
-  // lane-constant parts of the transpose-read addresses (PV A operand)
-  const int vrow_st = C::VST;
-  const int voff = C::OFF_V;
-  int tr_off[4];
-  {
-    const int G = lane >> 4, m = (lane & 15) >> 1, oo = lane & 1;
-#pragma unroll
-    for (int cc = 0; cc < 4; ++cc) {
-      const int k = 8 * cc + m;  // K-slot of this lane half
-      const int T = 32 * (k >> 4) + 8 * ((k >> 2) & 3) + 4 * hh + (k & 3);
-      tr_off[cc] = voff + T * vrow_st + 16 * (G & 1) + 8 * oo;
-    }
-  }
-
-  // O^T accumulates sum_n V_n 2^(s_n - m_ref) against a fixed per-lane (head)
-  // reference, the first tile's ceil(max); a tile's own offset rides on the
-  // B-operand e8m0 scale of the PV MFMA, so the accumulators are never
-  // rescaled.  A tile whose max lies more than kRebase above m_ref (the
-  // accumulators could overflow) makes the whole block restart the item with
-  // m_ref = the running max: a block-wide vote through LDS, one tile late.
-  uint8_t* vote = smem + C::OFF_VOTE;  // [2][4] wave flags, double-buffered by tile parity
-  float m_seen = neg_inf();
-  bool have_ref = false;
-  for (;;) {
-  if (ntiles > 0) prologue();
-  bool restart = false;
-  for (int ti = 0; ti < ntiles; ++ti) {
-    const int st = ti % C::S;
-    const int nval = min(kTile, ntok - kTile * ti);
-    // tile ti and its scales landed (and the slots of the tile issued next)
-    wait_vmcnt<0>();
-#pragma unroll
-    for (int u = 0; u < 2; ++u)
-#pragma unroll
-      for (int ks = 0; ks < 9; ++ks) sc_cur[u][ks] = sc_nxt[u][ks];
-    lds_barrier();  // tile ti visible; the stage of tile ti-1 is free
-    if (ti > 0 && __builtin_amdgcn_readfirstlane(*reinterpret_cast<const uint32_t*>(vote + 4 * ((ti - 1) & 1))) != 0) {
-      restart = true;
-      break;
-    }
-    if (ti + C::S - 1 < ntiles) {
-      issue_slots(ti + C::S);
-      issue_rows(ti + C::S - 1);
-      load_scales(ti + C::S - 1);
-    }
-
-    // ---- scores S^T: s0 = tokens 0..31, s1 = tokens 32..63 of the tile ------------
-    const uint8_t* kt = smem + st * C::STAGE;
-    v16f s0 = v16f{}, s1 = v16f{};
-    // one K-step of lookahead on the LDS fragments; sched_barrier keeps the
-    // compiler from hoisting every fragment load (register blow-up)
-    auto kfrag = [&](int ks, int u) -> v8i {
-      return ld_v4_as_v8(kt + (32 * u + l32) * C::KST + 16 * (2 * ks + hh));
-    };
-    v8i a0n = kfrag(0, 0), a1n = kfrag(0, 1);
-#pragma unroll
-    for (int ks = 0; ks < 9; ++ks) {
-      const v8i a0 = a0n, a1 = a1n;
-      if (ks < 8) {
-        a0n = kfrag(ks + 1, 0);
-        a1n = kfrag(ks + 1, 1);
-      }
-      s0 = mfma32_f4f8(a0, (int)sc_cur[0][ks], qv[ks], s0);
-      s1 = mfma32_f4f8(a1, (int)sc_cur[1][ks], qv[ks], s1);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    // s_u[r] = raw score(token 32u + 8(r/4) + 4hh + r%4, head); masked on a partial tile
-    if (nval < kTile) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int tk = 8 * (r >> 2) + 4 * hh + (r & 3);
-        if (tk >= nval) s0[r] = neg_inf();
-        if (32 + tk >= nval) s1[r] = neg_inf();
-      }
-    }
-    float mx0 = neg_inf(), mx1 = neg_inf();
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      mx0 = fmaxf(mx0, s0[r]);
-      mx1 = fmaxf(mx1, s1[r]);
-    }
-    mx0 = fmaxf(mx0, shfl_xor_f(mx0, 32));
-    mx1 = fmaxf(mx1, shfl_xor_f(mx1, 32));
-    // Per-item reference m_ref (the first tile's ceil max) and per-half offsets
-    // m_u = ceil(c max_u) (c > 0: the quantization scales are positive).  Half u
-    // is K block u of the PV MFMA, whose e8m0 B scale comes from lane group u
-    // (hh = u), so each half carries 2^(m_u - m_ref - 8) and O^T is never
-    // rescaled: O^T accumulates sum_n V_n 2^(s_n - m_ref).
-    const float m0 = __builtin_ceilf(mx0 * c), m1 = __builtin_ceilf(mx1 * c);  // -inf: empty half
-    const float mt = fmaxf(m0, m1);
-    if (!have_ref) m_ref = mt;  // first tile of the first pass
-    have_ref = true;
-    m_seen = fmaxf(m_seen, mt);
-    const bool over = __any(mt > m_ref + kRebase);
-    if (lane == 0) vote[4 * (ti & 1) + w] = over ? 1 : 0;
-    const float e0 = m0 == neg_inf() ? m_ref : m0, e1 = m1 == neg_inf() ? m_ref : m1;
-    const float d0 = fminf(fmaxf(e0 - m_ref, -160.f), 160.f), d1 = fminf(fmaxf(e1 - m_ref, -160.f), 160.f);
-    const int pscale = min(max((int)(hh ? d1 : d0) - 8 + 127, 0), 254);
-    // P'_u = 2^(c s - m_u + 8), fp8 hi + lo terms
-    float ps0 = 0.f, ps1 = 0.f;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      s0[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[r], c, 8.f - e0));
-      s1[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[r], c, 8.f - e1));
-      ps0 += s0[r];
-      ps1 += s1[r];
-    }
-    l_run += ps0 * __builtin_amdgcn_exp2f(d0 - 8.f) + ps1 * __builtin_amdgcn_exp2f(d1 - 8.f);
-    // P'^T B operand: byte 16u + 4q + i <-> token 32u + 8q + 4hh + i; hi + lo fp8 terms
-    v8i pbh, pbl;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      uint32_t h0, l0, h1, l1;
-      pack4_fp8_split(s0[4 * q], s0[4 * q + 1], s0[4 * q + 2], s0[4 * q + 3], h0, l0);
-      pack4_fp8_split(s1[4 * q], s1[4 * q + 1], s1[4 * q + 2], s1[4 * q + 3], h1, l1);
-      pbh[q] = (int)h0;
-      pbl[q] = (int)l0;
-      pbh[4 + q] = (int)h1;
-      pbl[4 + q] = (int)l1;
-    }
-    // ---- O^T += V^T . P^T, V^T fragments by transpose reads of the row tile ------
-    auto vfrag = [&](int dt) -> v8i {
-      const uint32_t vb = lds0 + st * C::STAGE + 32 * dt;
-      const v2i r0 = lds_read_tr8(vb + tr_off[0]);
-      const v2i r1 = lds_read_tr8(vb + tr_off[1]);
-      const v2i r2 = lds_read_tr8(vb + tr_off[2]);
-      const v2i r3 = lds_read_tr8(vb + tr_off[3]);
-      return v8i{r0[0], r0[1], r1[0], r1[1], r2[0], r2[1], r3[0], r3[1]};
-    };
-    // dims in pairs of 32-row tiles so the hi and lo MFMAs of one accumulator
-    // are not back to back; one pair of fragments read ahead
-    v8i an0 = vfrag(0), an1 = vfrag(1);
-#pragma unroll
-    for (int dt = 0; dt < 16; dt += 2) {
-      const v8i a0 = an0, a1 = an1;
-      if (dt < 14) {
-        an0 = vfrag(dt + 2);
-        an1 = vfrag(dt + 3);
-      }
-      o[dt] = mfma32_f8_bscale(a0, pbh, pscale, o[dt]);
-      o[dt + 1] = mfma32_f8_bscale(a1, pbh, pscale, o[dt + 1]);
-      o[dt] = mfma32_f8_bscale(a0, pbl, pscale, o[dt]);
-      o[dt + 1] = mfma32_f8_bscale(a1, pbl, pscale, o[dt + 1]);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  }
-  if (!restart && ntiles > 0) {
-    lds_barrier();  // the last tile's votes
-    restart = __builtin_amdgcn_readfirstlane(*reinterpret_cast<const uint32_t*>(vote + 4 * ((ntiles - 1) & 1))) != 0;
-  }
-  if (!restart) break;
-  // drain the ring (the prologue reuses it), then start over from m_ref = running max
-  wait_vmcnt<0>();
-  lds_barrier();
-  m_ref = m_seen;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) o[i] = v16f{};
-  l_run = 0.f;
-  }
-
-  // ---- finish ---------------------------------------------------------------------
-  const float L = l_run + shfl_xor_f(l_run, 32);
-  const float inv = L > 0.f ? vscale / L : 0.f;
-  if (slot < 0) {
-    if (p.lse_out != nullptr && hh == 0)
-      p.lse_out[(int64_t)b * 128 + head] = L > 0.f ? (m_ref + __log2f(L)) * kLn2 : neg_inf();
-    uint16_t* orow = p.out + ((int64_t)b * 128 + head) * kVDim;
-#pragma unroll
-    for (int dt = 0; dt < 16; ++dt) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int d = 32 * dt + 8 * q + 4 * hh;
-        const uint32_t lo = f32_to_bf16_bits(o[dt][4 * q] * inv) | (f32_to_bf16_bits(o[dt][4 * q + 1] * inv) << 16);
-        const uint32_t hi = f32_to_bf16_bits(o[dt][4 * q + 2] * inv) | (f32_to_bf16_bits(o[dt][4 * q + 3] * inv) << 16);
-        *reinterpret_cast<uint2*>(orow + d) = make_uint2(lo, hi);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  } else {
-    uint16_t* prow = p.part_o + ((int64_t)slot * 128 + head) * kVDim;
-#pragma unroll
-    for (int dt = 0; dt < 16; ++dt) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int d = 32 * dt + 8 * q + 4 * hh;
-        const uint32_t lo = f32_to_bf16_bits(o[dt][4 * q] * inv) | (f32_to_bf16_bits(o[dt][4 * q + 1] * inv) << 16);
-        const uint32_t hi = f32_to_bf16_bits(o[dt][4 * q + 2] * inv) | (f32_to_bf16_bits(o[dt][4 * q + 3] * inv) << 16);
-        *reinterpret_cast<uint2*>(prow + d) = make_uint2(lo, hi);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    if (hh == 0) p.part_lse[(int64_t)slot * 128 + head] = L > 0.f ? m_ref + __log2f(L) : neg_inf();
-  }
-}
-
-// ============================================================================
 // LSE combine: out[b,h,:] = sum_s 2^(lse_s - M) O_s / sum_s 2^(lse_s - M)
 // grid (batch, H/16, 4): block = 16 heads x 128 dims, thread = (head, 8 dims);
 // the split partials are read in batches of 8 so their loads overlap
@@ -1180,7 +833,7 @@ static hipError_t launch_decode_t(const DecodeParams& p, int kv_mode, int grid, 
     if (QB) return hipErrorInvalidValue;  // the H = 128 kernel takes a quantized Q
     switch (kv_mode) {
       case 0: return launch_decode_h128f(p, grid, stream);
-      case 2: hipLaunchKernelGGL((decode_h128_kernel<IDX>), dim3(grid), dim3(256), 0, stream, p); break;
+      case 2: return launch_decode_h128m(p, grid, stream);
       default: return hipErrorInvalidValue;
     }
   } else {

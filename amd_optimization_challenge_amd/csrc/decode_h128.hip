@@ -1,5 +1,7 @@
-// MLA absorbed decode, 128 heads with the fp8 cache (K = V = the 576-byte
-// rows), for gfx950.
+// MLA absorbed decode, 128 heads, for gfx950: the fp8 cache (K = V = the
+// 576-byte rows), and the two-cache mode (mxfp4 K rows with their e8m0 block
+// scales for QK, the fp8 cache's rows for V), which differs only in its LDS
+// rings, its DMA schedule and its QK operands (see the end of this comment).
 //
 // Work split: one work-group of 4 waves per CU runs one work item {batch,
 // token range, slot} of the on-device plan.  Wave w owns heads 32w .. 32w+31
@@ -47,6 +49,20 @@
 // wave makes the work-group run the item again with every head's m_ref set to
 // its running max over the whole item, which no tile then exceeds.
 //
+// Two-cache mode: K and V rows come from different caches, so they have rings
+// of their own, each sized to its lifetime: K rows (288 bytes of fp4, rows of
+// 304 bytes, conflict-free for the 16-byte fragment reads) in 3 pair stages;
+// V half rows (dims 256h .. +255, rows of 272 bytes, at their bank floor for
+// the transpose reads, which then need one address register) in 4 half-pair
+// stages, fetched one pair after their K (each half one iteration before its
+// stage is needed); the 18 e8m0 bytes of each K row in 3 stages, one byte per
+// dword (byte DMAs), placed so that a lane's 9 scales of a tile are three LDS
+// reads.  Every DMA of a pair has its own slot, and every pair issues all of
+// them (past the item's end they re-fetch its last row), so each wave's
+// outstanding-DMA count at the two barriers is a compile-time constant.  QK is
+// the scaled f8f6f4 MFMA with fp4 A (K, 4 VGPRs), the lane's e8m0 byte as A
+// scale, and fp8 Q^T in the order that pairs with the fp4 K layout.
+//
 // Behavioural reference: mixed-mla/asm_dumps/aiter_mla.py:149-470 (interface,
 // 128-head folding :318-353), TASK/reference.py:349-369 (numerics).
 #include <type_traits>
@@ -73,7 +89,30 @@ struct G128 {
   static constexpr int OFF_SLOT = NP * PSTAGE;
   static constexpr int OFF_FLAG = OFF_SLOT + NSL * 256;  // [4] per-wave overflow flags
   static constexpr int LDS = OFF_FLAG + 16;
+  static constexpr int OFF_Q = 2 * PSTAGE;      // Q (prologue): pair stages 2-3
   static_assert(WIN == 38 && DMAX == 10, "DMA window split");
+  static_assert(LDS <= 160 * 1024, "LDS");
+};
+
+// LDS of the two-cache mode (one pair = 64 rows per stage)
+struct M128 {
+  static constexpr int HT = 32;
+  static constexpr int KST = 304;                 // fp4 K row: 18 chunks + 1 of padding
+  static constexpr int KSTAGE = 2 * HT * KST;     // 19 one-KiB DMA windows
+  static constexpr int NK = 3;                    // K stages: pairs q (QK), q + 1, q + 2
+  static constexpr int VST = 272;                 // fp8 V half row: 16 chunks + 1 of padding
+  static constexpr int VSTAGE = 2 * HT * VST;     // 17 one-KiB windows
+  static constexpr int NV = 4;                    // V half stages
+  static constexpr int SSTAGE = 2 * HT * 18 * 4;  // e8m0 bytes, one per dword: 18 256-byte windows
+  static constexpr int NSL = 8;                   // slot stages (one per pair)
+  static constexpr int OFF_V = NK * KSTAGE;
+  static constexpr int OFF_S = OFF_V + NV * VSTAGE;
+  static constexpr int OFF_SLOT = OFF_S + NK * SSTAGE;
+  static constexpr int OFF_FLAG = OFF_SLOT + NSL * 256;
+  static constexpr int LDS = OFF_FLAG + 16;
+  static constexpr int OFF_Q = 2 * KSTAGE;        // Q (prologue): K stage 2 and the V stages
+  static_assert(KSTAGE == 19 * 1024 && VSTAGE == 17 * 1024 && SSTAGE == 18 * 256, "DMA windows");
+  static_assert(OFF_Q + 128 * kQKDim <= OFF_S, "Q staging stays clear of the e8m0 stages");
   static_assert(LDS <= 160 * 1024, "LDS");
 };
 
@@ -85,6 +124,15 @@ __device__ __forceinline__ int g128_pos(int r, int c) {
 }
 
 __device__ __forceinline__ float ninf() { return -__builtin_inff(); }
+
+// s_waitcnt vmcnt(N_w) for wave w (wave-uniform branch)
+template <int N0, int N1, int N2, int N3>
+__device__ __forceinline__ void wait_vmcnt_w(int w) {
+  if (w == 0) wait_vmcnt<N0>();
+  else if (w == 1) wait_vmcnt<N1>();
+  else if (w == 2) wait_vmcnt<N2>();
+  else wait_vmcnt<N3>();
+}
 
 // QK: 32x32x64 fp8 MFMA with its accumulator in VGPRs (O^T holds all AGPRs, and
 // the builtin would give every MFMA of the kernel an AGPR accumulator).  All
@@ -100,6 +148,20 @@ __device__ __forceinline__ void qk_first(v16f& d, const v8i& a, const v8i& b) {
 }
 __device__ __forceinline__ void qk_acc(v16f& d, const v8i& a, const v8i& b) {
   asm volatile("s_nop 1\n\tv_mfma_f32_32x32x64_f8f6f4 %0, %1, %2, %0\n\ts_nop 2" : "+v"(d) : "v"(a), "v"(b));
+}
+// the same with fp4 A (4 VGPRs: 32 e2m1 values) at the lane's e8m0 scale sa
+// (byte 0), fp8 B at unit scale
+__device__ __forceinline__ void qk4_first(v16f& d, const v4i& a, const v8i& b, int sa) {
+  asm volatile(
+      "s_nop 1\n\tv_mfma_scale_f32_32x32x64_f8f6f4 %0, %1, %2, 0, %3, %4 op_sel_hi:[0,0,0] cbsz:4\n\ts_nop 2"
+      : "=&v"(d)
+      : "v"(a), "v"(b), "v"(sa), "v"(127));
+}
+__device__ __forceinline__ void qk4_acc(v16f& d, const v4i& a, const v8i& b, int sa) {
+  asm volatile(
+      "s_nop 1\n\tv_mfma_scale_f32_32x32x64_f8f6f4 %0, %1, %2, %0, %3, %4 op_sel_hi:[0,0,0] cbsz:4\n\ts_nop 2"
+      : "+v"(d)
+      : "v"(a), "v"(b), "v"(sa), "v"(127));
 }
 __device__ __forceinline__ void drain_v(v16f& x) { asm volatile("s_nop 15\n\ts_nop 15" : "+v"(x)); }
 // PV: O^T += V^T . P'^T with an e8m0 scale on B (one per lane: its head), A at
@@ -207,10 +269,56 @@ struct H128Sched {
   static constexpr int kBarrier = 45;
 };
 
-template <bool IDX>
-__global__ __launch_bounds__(256, 1) void decode_h128f_kernel(const DecodeParams p) {
-  using C = G128;
+// The two-cache mode's DMAs of pair q, one per pair slot, each window's slot
+// index read two slots before: V(q) half 0 (type 0) at slots 3 + 4m, half 1
+// (type 1) at 24 + 4m, K(q + 2) rows (type 2) at 5, 13, 22, 30, 38, their e8m0
+// bytes (type 3) at 9, 17, 26, 34, 42; window m of a type is the wave's
+// window w + 4m of the stage.  Half 0 goes into the stage freed at the
+// barrier that ends pair q - 1, half 1 into the one freed at slot 20; K and
+// e8m0 into the stage of pair q - 1, free since that barrier too.
+struct MixSched {
+  static constexpr int at(int type, int m) {
+    return type == 0 ? 3 + 4 * m : type == 1 ? 24 + 4 * m : type == 2 ? (m < 2 ? 5 + 8 * m : 6 + 8 * m)
+                                                                       : (m < 2 ? 9 + 8 * m : 10 + 8 * m);
+  }
+  // 8 type + m of the DMA at pair slot s, or -1
+  static constexpr int dma(int s) {
+    for (int ty = 0; ty < 4; ++ty)
+      for (int m = 0; m < 5; ++m)
+        if (at(ty, m) == s) return 8 * ty + m;
+    return -1;
+  }
+  static constexpr int read(int s) {
+    for (int ty = 0; ty < 4; ++ty)
+      for (int m = 0; m < 5; ++m)
+        if (at(ty, m) - 2 == s) return 8 * ty + m;
+    return -1;
+  }
+  // windows per stage: V 17, K 19, e8m0 18; wave w has the fifth (m = 4) iff
+  // w + 16 is one of them
+  static constexpr bool has(int type, int m, int w) { return m < 4 || w < (type < 2 ? 1 : type == 2 ? 3 : 2); }
+  // DMAs wave w issues at pair slots [lo, hi) (with the slot-index DMA of wave 0)
+  static constexpr int issued(int w, bool idx, int lo, int hi) {
+    int c = (idx && w == 0 && lo <= H128Sched::kSlotDma && H128Sched::kSlotDma < hi) ? 1 : 0;
+    for (int ty = 0; ty < 4; ++ty)
+      for (int m = 0; m < 5; ++m)
+        if (has(ty, m, w) && lo <= at(ty, m) && at(ty, m) < hi) ++c;
+    return c;
+  }
+  // outstanding DMAs allowed at the slot-20 barrier (V(q - 1) half 0 landed:
+  // it publishes that half) and at the slot-45 barrier (every DMA of pair q - 1
+  // landed: V(q - 1) half 1, K(q + 1), e8m0(q + 1))
+  static constexpr int left_free(int w, bool idx) { return issued(w, idx, 20, 50) + issued(w, idx, 0, 20); }
+  static constexpr int left_pub(int w, bool idx) { return issued(w, idx, 43, 50) + issued(w, idx, 0, 45); }
+  static_assert(H128Sched::kStageFree == 20 && H128Sched::kBarrier == 45, "barrier slots");
+};
+
+// MIX: the two-cache mode (fp4 K + e8m0, fp8 V); else the fp8 cache
+template <bool IDX, bool MIX>
+__global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams p) {
+  using C = std::conditional_t<MIX, M128, G128>;
   using SC = H128Sched;
+  using MS = MixSched;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[C::LDS];
   const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
 
@@ -244,45 +352,76 @@ __global__ __launch_bounds__(256, 1) void decode_h128f_kernel(const DecodeParams
     }
   };
   // ---- Q: wave w's 32 head rows (18 KiB, contiguous in memory) go by LDS-DMA
-  // into pair stages 2-3, which the first rows(2) DMA overwrites only after the
-  // barrier that follows the Q^T register reads; Q then needs no compiler-
-  // tracked global load (whose conservative wait would also drain the row DMAs)
+  // into ring stages that the pipeline first writes only after the barrier
+  // that follows the Q^T register reads (pair stages 2-3; in the two-cache
+  // mode K stage 2 and the V stages); Q then needs no compiler-tracked global
+  // load (whose conservative wait would also drain the row DMAs)
   constexpr int kQWin = 32 * kQKDim / 1024;  // 18 one-KiB windows per wave
-  const uint32_t q_lds = lds0 + 2 * C::PSTAGE + w * 32 * kQKDim;
+  const uint32_t q_lds = lds0 + C::OFF_Q + w * 32 * kQKDim;
   auto issue_q = [&]() __attribute__((always_inline)) {
     const uint8_t* qsrc = p.q_fp8 + ((int64_t)b * 128 + 32 * w) * kQKDim + 16 * lane;
     asm volatile("" : "+v"(qsrc));  // the window addresses are formed here, not kept live from the entry
 #pragma unroll
     for (int k = 0; k < kQWin; ++k) dma16_to_lds(qsrc + 1024 * k, q_lds + 1024 * k);
   };
-  // Q^T B operand: K-step ks = dims 64ks .. +63 (lane half hh: 32hh .. +31)
+  // Q^T B operand: K-step ks = dims 64ks .. +63; lane half hh holds dims
+  // 32hh .. +31 (fp8 K) or, paired with fp4 K, dims 16hh .. +15 and 32 + 16hh
+  // .. +15 (the f8f6f4 MFMA pairs fp4 element e of lane half hh, K index 32hh
+  // + e, with fp8 byte i of lane half hh', K index 16hh' + (i & 15) + 32 (i >> 4))
   v8i qv[9];
   auto read_q = [&]() __attribute__((always_inline)) {
     typedef __attribute__((address_space(3))) v4i lds_v4i_q;
-    const uint32_t a = q_lds + l32 * kQKDim + 32 * hh;
+    const uint32_t a = q_lds + l32 * kQKDim + (MIX ? 16 : 32) * hh;
 #pragma unroll
     for (int ks = 0; ks < 9; ++ks) {
       const v4i lo = *(const lds_v4i_q*)(uintptr_t)(a + 64 * ks);
-      const v4i hi = *(const lds_v4i_q*)(uintptr_t)(a + 64 * ks + 16);
+      const v4i hi = *(const lds_v4i_q*)(uintptr_t)(a + 64 * ks + (MIX ? 32 : 16));
       qv[ks] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     }
   };
-  const float c = p.q_scale[0] * p.kv_scale[0] * p.sm_scale * kLog2eF;
+  // fp4 K: its e8m0 block scales ride on the QK MFMA's A scale
+  const float c = p.q_scale[0] * (MIX ? 1.0f : p.kv_scale[0]) * p.sm_scale * kLog2eF;
   const float vscale = p.kv_scale[0];
 
   // ---- DMA maps ---------------------------------------------------------------
-  // window u = w + 4k of a pair stage puts lane l at chunk position 64u + l =
-  // (row r of the pair, position j); it fetches logical chunk g128_pos(r, j)
-  // (chunk 0 for the two padding positions); packed (r << 10 | byte offset),
-  // two windows per register
-  uint32_t dmap[C::DMAX / 2];
+  // fp8 cache: window u = w + 4k of a pair stage puts lane l at chunk position
+  // 64u + l = (row r of the pair, position j); it fetches logical chunk
+  // g128_pos(r, j) (chunk 0 for the two padding positions); packed (r << 10 |
+  // byte offset), two windows per register.
+  // Two-cache mode: window m of each type (the wave's window u = w + 4m of the
+  // stage) puts lane l at position e = 64u + l: K, chunk e of the stage = row
+  // e / 19, chunk e % 19 (the padding chunk re-fetches chunk 0); V half, row e /
+  // 17, chunk e % 17 (likewise); e8m0, dword e = row r, byte 2ks + hh at 16r +
+  // 8hh + ks (ks < 8), byte 16 + hh at 1024 + 64hh + r.  Packed (r << 9 | source
+  // byte offset in the row), entries K 0..4, e8m0 5..9, V 10..14.
+  constexpr int kMaps = MIX ? 8 : G128::DMAX / 2;
+  uint32_t dmap[kMaps];
+  if constexpr (MIX) {
+    uint32_t ent[16];
 #pragma unroll
-  for (int k = 0; k < C::DMAX; ++k) {
-    const int pidx = min(64 * (w + 4 * k) + lane, 64 * C::WIN - 1);
-    const int r = pidx / C::CPR, j = pidx - C::CPR * r;
-    const uint32_t e = ((uint32_t)r << 10) | (uint32_t)(16 * (j < 36 ? g128_pos(r, j) : 0));
-    if (k % 2 == 0) dmap[k / 2] = e;
-    else dmap[k / 2] |= e << 16;
+    for (int m = 0; m < 5; ++m) {
+      const int e = 64 * (w + 4 * m) + lane;
+      const int rk = min(e / 19, 63), ck = e - 19 * (e / 19);
+      ent[m] = ((uint32_t)rk << 9) | (uint32_t)(16 * (ck < 18 ? ck : 0));
+      const int e2 = e - 1024;
+      const int rs_ = e < 1024 ? e >> 4 : e2 & 63;
+      const int js = e < 1024 ? 2 * (e & 7) + ((e >> 3) & 1) : 16 + ((e2 >> 6) & 1);
+      ent[5 + m] = ((uint32_t)rs_ << 9) | (uint32_t)js;
+      const int rv = min(e / 17, 63), cv = e - 17 * (e / 17);
+      ent[10 + m] = ((uint32_t)rv << 9) | (uint32_t)(16 * (cv < 16 ? cv : 0));
+    }
+    ent[15] = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) dmap[k] = ent[2 * k] | (ent[2 * k + 1] << 16);
+  } else {
+#pragma unroll
+    for (int k = 0; k < G128::DMAX; ++k) {
+      const int pidx = min(64 * (w + 4 * k) + lane, 64 * G128::WIN - 1);
+      const int r = pidx / G128::CPR, j = pidx - G128::CPR * r;
+      const uint32_t e = ((uint32_t)r << 10) | (uint32_t)(16 * (j < 36 ? g128_pos(r, j) : 0));
+      if (k % 2 == 0) dmap[k / 2] = e;
+      else dmap[k / 2] |= e << 16;
+    }
   }
   // Window k of pair rq: its slot (read from the pair's slot-ring stage at
   // sbase) and its DMA into the pair's stage (stage_w: the stage plus 1 KiB w;
@@ -300,7 +439,7 @@ __global__ __launch_bounds__(256, 1) void decode_h128f_kernel(const DecodeParams
     }
   };
   auto row_dma = [&](int k, int sl, uint32_t stage_w) __attribute__((always_inline)) {
-    if (k < C::DMAX - 1 || w < 2) {
+    if (k < G128::DMAX - 1 || w < 2) {
       uint32_t d = dmap[k / 2];
       asm volatile("" : "+v"(d));
       const uint32_t off = (d >> (16 * (k % 2))) & 1023u;
@@ -312,26 +451,26 @@ __global__ __launch_bounds__(256, 1) void decode_h128f_kernel(const DecodeParams
     }
   };
   auto stage_of = [&](int q) __attribute__((always_inline)) -> uint32_t {  // pair q's stage + 1 KiB w
-    return __builtin_amdgcn_readfirstlane(lds0 + (q % C::NP) * C::PSTAGE + 1024 * w);
+    return __builtin_amdgcn_readfirstlane(lds0 + (q % G128::NP) * G128::PSTAGE + 1024 * w);
   };
   auto sring_of = [&](int q) __attribute__((always_inline)) -> uint32_t {  // pair q's slot-ring stage
     return __builtin_amdgcn_readfirstlane(lds0 + C::OFF_SLOT + (q % C::NSL) * 256);
   };
   auto issue_rows = [&](int q) __attribute__((always_inline)) {
     const uint32_t stw = stage_of(q), sb = sring_of(q);
-    int sl[C::DMAX];
+    int sl[G128::DMAX];
 #pragma unroll
-    for (int k = 0; k < C::DMAX; ++k) sl[k] = row_slot(k, q, sb);  // every read before the first DMA
+    for (int k = 0; k < G128::DMAX; ++k) sl[k] = row_slot(k, q, sb);  // every read before the first DMA
 #pragma unroll
-    for (int k = 0; k < C::DMAX; ++k) row_dma(k, sl[k], stw);
+    for (int k = 0; k < G128::DMAX; ++k) row_dma(k, sl[k], stw);
   };
   // rows(q) have landed once the DMAs issued after them are all that is
   // outstanding: the next pair's slot indices (wave 0) and its rows (ten
   // windows for waves 0 and 1, nine for waves 2 and 3)
   auto wait_rows = [&]() __attribute__((always_inline)) {
-    if (w == 0) wait_vmcnt<IDX ? C::DMAX + 1 : C::DMAX>();
-    else if (w == 1) wait_vmcnt<C::DMAX>();
-    else wait_vmcnt<C::DMAX - 1>();
+    if (w == 0) wait_vmcnt<IDX ? G128::DMAX + 1 : G128::DMAX>();
+    else if (w == 1) wait_vmcnt<G128::DMAX>();
+    else wait_vmcnt<G128::DMAX - 1>();
   };
   // the same near the end of the item, where no rows follow (only the slot
   // indices of wave 0)
@@ -339,25 +478,92 @@ __global__ __launch_bounds__(256, 1) void decode_h128f_kernel(const DecodeParams
     if (IDX && w == 0) wait_vmcnt<1>();
     else wait_vmcnt<0>();
   };
+  // two-cache mode: the slot of map entry k's row in pair pq (ring stage sbase)
+  auto mix_slot = [&](int k, int pq, uint32_t sbase) __attribute__((always_inline)) -> int {
+    uint32_t d = dmap[k / 2];
+    asm volatile("" : "+v"(d));
+    const uint32_t e = (d >> (16 * (k % 2))) & 0xFFFFu;
+    if constexpr (IDX) {
+      typedef __attribute__((address_space(3))) int lds_int;
+      return *(const lds_int*)(uintptr_t)(sbase + ((e >> 7) & ~3u));  // 4r
+    } else {
+      return min(t_beg + 64 * pq + (int)(e >> 9), t_end - 1);
+    }
+  };
+  // window m of type ty (0, 1: V half; 2: K; 3: e8m0) from slot sl into the
+  // stage at base (the stage plus this wave's first window)
+  auto mix_dma = [&](int ty, int m, int sl, uint32_t base) __attribute__((always_inline)) {
+    if (MS::has(ty, m, w)) {
+      const int k = ty < 2 ? 10 + m : ty == 2 ? m : 5 + m;
+      uint32_t d = dmap[k / 2];
+      asm volatile("" : "+v"(d));
+      const uint32_t off = (d >> (16 * (k % 2))) & 511u;
+      if (ty == 3) {
+        const uint8_t* src = p.k_scales + ((uint64_t)(uint32_t)sl * (uint32_t)p.k_scale_stride + off);
+        asm volatile("s_add_u32 m0, %0, %1\n\tglobal_load_lds_ubyte %2, off"
+                     :
+                     : "s"(base), "i"(1024 * m), "v"(src)
+                     : "memory", "m0");
+      } else {
+        const uint8_t* src = ty == 2 ? p.k_cache + ((uint64_t)(uint32_t)sl * (uint32_t)p.k_row_stride + off)
+                                     : p.v_cache + ((uint64_t)(uint32_t)sl * (uint32_t)p.v_row_stride +
+                                                    (uint32_t)(256 * ty) + off);
+        asm volatile("s_add_u32 m0, %0, %1\n\tglobal_load_lds_dwordx4 %2, off"
+                     :
+                     : "s"(base), "i"(4096 * m), "v"(src)
+                     : "memory", "m0");
+      }
+    }
+  };
+  auto kstage_of = [&](int x) __attribute__((always_inline)) -> uint32_t {  // K stage of pair x + 1 KiB w
+    return __builtin_amdgcn_readfirstlane(lds0 + (x % M128::NK) * M128::KSTAGE + 1024 * w);
+  };
+  auto sstage_of = [&](int x) __attribute__((always_inline)) -> uint32_t {  // e8m0 stage + 256 w
+    return __builtin_amdgcn_readfirstlane(lds0 + M128::OFF_S + (x % M128::NK) * M128::SSTAGE + 256 * w);
+  };
+  auto vstage_of = [&](int hx) __attribute__((always_inline)) -> uint32_t {  // half stage hx & 3 + 1 KiB w
+    return __builtin_amdgcn_readfirstlane(lds0 + M128::OFF_V + (hx & 3) * M128::VSTAGE + 1024 * w);
+  };
+  // K rows and e8m0 bytes of pair x (the prologue), every slot read first
+  auto mix_issue_ks = [&](int x) __attribute__((always_inline)) {
+    const uint32_t sb = sring_of(x), kb = kstage_of(x), eb = sstage_of(x);
+    int sl[10];
+#pragma unroll
+    for (int k = 0; k < 10; ++k) sl[k] = mix_slot(k, x, sb);
+#pragma unroll
+    for (int m = 0; m < 5; ++m) mix_dma(2, m, sl[m], kb);
+#pragma unroll
+    for (int m = 0; m < 5; ++m) mix_dma(3, m, sl[5 + m], eb);
+  };
 
   // ---- lane-constant fragment offsets -----------------------------------------
-  // K fragment (QK A operand) of K-step ks: row l32 of the tile, logical chunks
-  // 4ks + 2hh + {0, 1} (ks < 8) or 32 + 2hh + {0, 1} (ks = 8).  Rows r and r + 32
-  // share a key, so the offsets hold for both tiles of a pair.
+  // fp8 cache.  K fragment (QK A operand) of K-step ks: row l32 of the tile,
+  // logical chunks 4ks + 2hh + {0, 1} (ks < 8) or 32 + 2hh + {0, 1} (ks = 8).
+  // Rows r and r + 32 share a key, so the offsets hold for both tiles of a pair.
   // ka[2 (ks & 1) + j] + 128 (ks >> 1) (ks < 8), ka[4 + j] (ks = 8): LDS
   // addresses of the current K tile, moved along the ring in place.
-  uint32_t ka[6];
+  // Two-cache mode.  K fragment of step ks: chunk 2ks + hh of row l32 of the
+  // tile, at ka[0] + 32ks; the tile's e8m0 bytes: ks < 8 at ka[1] + 4ks (two
+  // 16-byte reads), ks = 8 at ka[2].
+  uint32_t ka[MIX ? 3 : 6];
   // (the init lambdas derive everything from an opaque copy of the lane id, so
   // the addresses are formed where they are needed, not kept live from the entry)
   auto init_ka = [&]() __attribute__((always_inline)) {
     int ln = lane;
     asm volatile("" : "+v"(ln));
-    const int r = ln & 31, h2 = (ln >> 5) * 2, x = g128_key(r);
+    if constexpr (MIX) {  // pair 0: stage 0, tile 0
+      const int r = ln & 31, h = ln >> 5;
+      ka[0] = lds0 + r * M128::KST + 16 * h;
+      ka[1] = lds0 + M128::OFF_S + 64 * r + 32 * h;
+      ka[2] = lds0 + M128::OFF_S + 4096 + 256 * h + 4 * r;
+    } else {
+      const int r = ln & 31, h2 = (ln >> 5) * 2, x = g128_key(r);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      ka[j] = lds0 + r * C::RST + 16 * ((h2 + j) ^ x);
-      ka[2 + j] = lds0 + r * C::RST + 16 * ((4 + h2 + j) ^ x);
-      ka[4 + j] = lds0 + r * C::RST + 16 * (32 + ((h2 + j) ^ (x & 3)));
+      for (int j = 0; j < 2; ++j) {
+        ka[j] = lds0 + r * G128::RST + 16 * ((h2 + j) ^ x);
+        ka[2 + j] = lds0 + r * G128::RST + 16 * ((4 + h2 + j) ^ x);
+        ka[4 + j] = lds0 + r * G128::RST + 16 * (32 + ((h2 + j) ^ (x & 3)));
+      }
     }
   };
   // V^T fragment (PV A operand) of dim tile dt (dims 32dt .. +31) over the 64
@@ -365,42 +571,77 @@ __global__ __launch_bounds__(256, 1) void decode_h128f_kernel(const DecodeParams
   // row T0 + 16cc of the pair's first tile (bytes 8cc .. +7) and of its second
   // tile (bytes 16 + 8cc .. +7), T0 = 8(m >> 2) + 4hh + (m & 3), logical chunk
   // 2dt + (G & 1), byte 8oo: byte 16u + 4q + i <-> token 8q + 4hh + i of tile
-  // u, the order of the lane's own scores.  Row T0 + 16cc has key x0 ^ 4cc,
-  // x0 = T0 >> 2.  va[4cc + (dt & 3)] + 128 (dt >> 2) (+ TSTAGE): LDS
-  // addresses of the PV pair's first (second) tile.
-  uint32_t va[8];
+  // u, the order of the lane's own scores.  fp8 cache: row T0 + 16cc has key
+  // x0 ^ 4cc, x0 = T0 >> 2; va[4cc + (dt & 3)] + 128 (dt >> 2) (+ TSTAGE): LDS
+  // addresses of the PV pair's first (second) tile.  Two-cache mode: half rows
+  // of 17 chunks, unswizzled (the 16 rows T0 fall on 16 distinct chunk
+  // positions), so every read of dim tile 8h + g is va[0] + 32g + (32u + 16cc)
+  // 272, va[0] in the half stage of the iteration.
+  uint32_t va[MIX ? 1 : 8];
   auto init_va = [&]() __attribute__((always_inline)) {
     int ln = lane;
     asm volatile("" : "+v"(ln));
     const int G = ln >> 4, m = (ln & 15) >> 1, oo = ln & 1;
     const int T0 = 8 * (m >> 2) + 4 * (ln >> 5) + (m & 3);
-    const int x0 = T0 >> 2;
+    if constexpr (MIX) {  // iteration 0 reads half stage 1 (never by an MFMA)
+      va[0] = lds0 + M128::OFF_V + M128::VSTAGE + T0 * M128::VST + 16 * (G & 1) + 8 * oo;
+    } else {
+      const int x0 = T0 >> 2;
 #pragma unroll
-    for (int cc = 0; cc < 2; ++cc)
+      for (int cc = 0; cc < 2; ++cc)
 #pragma unroll
-      for (int e = 0; e < 4; ++e)  // pair -2: stage 2 (never read by an MFMA)
-        va[4 * cc + e] = lds0 + 2 * C::PSTAGE + (T0 + 16 * cc) * C::RST +
-                         16 * ((2 * e + (G & 1)) ^ (x0 ^ (4 * cc))) + 8 * oo;
+        for (int e = 0; e < 4; ++e)  // pair -2: stage 2 (never read by an MFMA)
+          va[4 * cc + e] = lds0 + 2 * G128::PSTAGE + (T0 + 16 * cc) * G128::RST +
+                           16 * ((2 * e + (G & 1)) ^ (x0 ^ (4 * cc))) + 8 * oo;
+    }
   };
   typedef __attribute__((address_space(3))) v4i lds_v4i;
+  typedef __attribute__((address_space(3))) int lds_i32;
   v8i kf[3];
-  v8i vf[2];
+  v4i kf4[3];                  // two-cache mode: fp4 K fragments
+  v4i sc_lo, sc_hi;            // two-cache mode: e8m0 of steps 0..3, 4..7
+  int sc8 = 127;               // and of step 8
   auto kload = [&](int g) __attribute__((always_inline)) {  // K fragment of step g (0..8) into kf[g % 3]
-    const uint32_t a0 = g < 8 ? ka[2 * (g & 1)] + 128 * (g >> 1) : ka[4];
-    const uint32_t a1 = g < 8 ? ka[2 * (g & 1) + 1] + 128 * (g >> 1) : ka[5];
-    const v4i lo = *(const lds_v4i*)(uintptr_t)a0;
-    const v4i hi = *(const lds_v4i*)(uintptr_t)a1;
-    kf[g % 3] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    if constexpr (MIX) {
+      kf4[g % 3] = *(const lds_v4i*)(uintptr_t)(ka[0] + 32 * g);
+    } else {
+      const uint32_t a0 = g < 8 ? ka[2 * (g & 1)] + 128 * (g >> 1) : ka[4];
+      const uint32_t a1 = g < 8 ? ka[2 * (g & 1) + 1] + 128 * (g >> 1) : ka[5];
+      const v4i lo = *(const lds_v4i*)(uintptr_t)a0;
+      const v4i hi = *(const lds_v4i*)(uintptr_t)a1;
+      kf[g % 3] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    }
   };
   // V^T fragment of group g (dim tile dt = 8h + g) into vf[g % 2]
+  v8i vf[2];
   auto vload = [&](int h, int g) __attribute__((always_inline)) {
-    const int dt = 8 * h + g;
-    const uint32_t a0 = va[dt & 3] + 128 * (dt >> 2), a1 = va[4 + (dt & 3)] + 128 * (dt >> 2);
-    const v2i r0 = lds_read_tr8(a0);
-    const v2i r1 = lds_read_tr8(a1);
-    const v2i r2 = lds_read_tr8(a0 + C::TSTAGE);
-    const v2i r3 = lds_read_tr8(a1 + C::TSTAGE);
-    vf[g % 2] = v8i{r0[0], r0[1], r1[0], r1[1], r2[0], r2[1], r3[0], r3[1]};
+    if constexpr (MIX) {
+      const uint32_t a = va[0] + 32 * g;
+      const v2i r0 = lds_read_tr8(a);
+      const v2i r1 = lds_read_tr8(a + 16 * M128::VST);
+      const v2i r2 = lds_read_tr8(a + 32 * M128::VST);
+      const v2i r3 = lds_read_tr8(a + 48 * M128::VST);
+      vf[g % 2] = v8i{r0[0], r0[1], r1[0], r1[1], r2[0], r2[1], r3[0], r3[1]};
+    } else {
+      const int dt = 8 * h + g;
+      const uint32_t a0 = va[dt & 3] + 128 * (dt >> 2), a1 = va[4 + (dt & 3)] + 128 * (dt >> 2);
+      const v2i r0 = lds_read_tr8(a0);
+      const v2i r1 = lds_read_tr8(a1);
+      const v2i r2 = lds_read_tr8(a0 + G128::TSTAGE);
+      const v2i r3 = lds_read_tr8(a1 + G128::TSTAGE);
+      vf[g % 2] = v8i{r0[0], r0[1], r1[0], r1[1], r2[0], r2[1], r3[0], r3[1]};
+    }
+  };
+  // two-cache mode: the e8m0 bytes of the current K tile (ka[1], ka[2])
+  auto scload_lo = [&]() __attribute__((always_inline)) { sc_lo = *(const lds_v4i*)(uintptr_t)ka[1]; };
+  auto scload_hi = [&]() __attribute__((always_inline)) { sc_hi = *(const lds_v4i*)(uintptr_t)(ka[1] + 16); };
+  auto scload_8 = [&]() __attribute__((always_inline)) { sc8 = *(const lds_i32*)(uintptr_t)ka[2]; };
+  // two-cache mode: outstanding-DMA waits of the two barriers
+  auto mix_wait_free = [&]() __attribute__((always_inline)) {
+    wait_vmcnt_w<MS::left_free(0, IDX), MS::left_free(1, IDX), MS::left_free(2, IDX), MS::left_free(3, IDX)>(w);
+  };
+  auto mix_wait_pub = [&]() __attribute__((always_inline)) {
+    wait_vmcnt_w<MS::left_pub(0, IDX), MS::left_pub(1, IDX), MS::left_pub(2, IDX), MS::left_pub(3, IDX)>(w);
   };
 
   v16f o[16];
@@ -484,6 +725,7 @@ __global__ __launch_bounds__(256, 1) void decode_h128f_kernel(const DecodeParams
   // tokens of its two tiles, whose softmax ended the iteration before.
   v16f sa, sb;  // QK accumulators of tiles of parity 0 / 1
   int rs[2] = {0, 0};  // slots of the next row DMAs (read two slots ahead)
+  int mrs = 0;         // two-cache mode: the same (one at a time)
   // GUARD: a pair at an edge of the pipeline, whose QK, softmax and PV parts
   // run only where their tile (pair) exists: t < n; 1 <= t <= n; pair j >= 0,
   // 2j < n.  Fragment loads and slot-index DMAs run everywhere (their
@@ -495,7 +737,18 @@ __global__ __launch_bounds__(256, 1) void decode_h128f_kernel(const DecodeParams
     constexpr int DM = decltype(dm_tag)::value;
     asm volatile("" : "+s"(q));  // nothing that depends on q is precomputed (and kept live) outside the pair
     const bool dmas = DM == 1 || (DM == 2 && q + 2 < npair);
-    const uint32_t stw = stage_of(q + 2), sring = sring_of(q + 2);
+    uint32_t stw = 0, sring = 0, sring_v = 0, kb = 0, eb = 0, vb0 = 0, vb1 = 0;
+    if constexpr (MIX) {  // K and e8m0 of pair q + 2, V halves of pair q
+      sring = sring_of(q + 2);
+      sring_v = sring_of(q);
+      kb = kstage_of(q + 2);
+      eb = sstage_of(q + 2);
+      vb0 = vstage_of(2 * q);
+      vb1 = vstage_of(2 * q + 1);
+    } else {
+      stw = stage_of(q + 2);
+      sring = sring_of(q + 2);
+    }
     static_for<0, 2 * SC::kSlots>([&](auto S) __attribute__((always_inline)) {
       constexpr int ps_ = decltype(S)::value;  // slot of the pair
       constexpr int IT = ps_ / SC::kSlots;      // iteration of the pair (tile t = 2q + IT)
@@ -515,8 +768,14 @@ __global__ __launch_bounds__(256, 1) void decode_h128f_kernel(const DecodeParams
       if constexpr (SC::is_qk(i)) {
         constexpr int g = i / 3;
         if (!GUARD || t < n) {
-          if constexpr (g == 0) qk_first(s_qk, kf[0], qv[0]);
-          else qk_acc(s_qk, kf[g % 3], qv[g]);
+          if constexpr (MIX) {
+            const int sa = g < 4 ? sc_lo[g & 3] : g < 8 ? sc_hi[g & 3] : sc8;
+            if constexpr (g == 0) qk4_first(s_qk, kf4[0], qv[0], sa);
+            else qk4_acc(s_qk, kf4[g % 3], qv[g], sa);
+          } else {
+            if constexpr (g == 0) qk_first(s_qk, kf[0], qv[0]);
+            else qk_acc(s_qk, kf[g % 3], qv[g]);
+          }
         }
       } else {
         constexpr int g = i / 3, term = i % 3 - 1;
@@ -524,9 +783,14 @@ __global__ __launch_bounds__(256, 1) void decode_h128f_kernel(const DecodeParams
       }
       // 2. barriers: pair q - 2's stage free (every wave's last V^T read of it
       // done); pair q + 1 published (its rows landed)
-      if constexpr (ps_ == SC::kStageFree) lds_barrier();
+      if constexpr (ps_ == SC::kStageFree) {
+        if constexpr (MIX) mix_wait_free();  // and V(q - 1) half 0 published
+        lds_barrier();
+      }
       if constexpr (ps_ == SC::kBarrier) {
-        if constexpr (DM == 1) {
+        if constexpr (MIX) {
+          mix_wait_pub();
+        } else if constexpr (DM == 1) {
           wait_rows();
         } else if constexpr (DM == 0) {
           wait_rows_last();
@@ -538,31 +802,67 @@ __global__ __launch_bounds__(256, 1) void decode_h128f_kernel(const DecodeParams
       }
       // 3. slot indices of pair q + 4, rows of pair q + 2
       if constexpr (ps_ == SC::kSlotDma) issue_slots(q + 4);
-      if constexpr (SC::row_dma(ps_) >= 0) {
-        constexpr int k = SC::row_dma(ps_);
-        if (dmas) row_dma(k, rs[k % 2], stw);
-      }
-      if constexpr (SC::row_read(ps_) >= 0) {
-        constexpr int k = SC::row_read(ps_);
-        if constexpr (DM != 0) rs[k % 2] = row_slot(k, q + 2, sring);
+      if constexpr (MIX) {  // every DMA of the pair, always (uniform vmcnt counts)
+        constexpr int ev = MS::dma(ps_);
+        if constexpr (ev >= 0) {
+          constexpr int ty = ev / 8, m = ev % 8;
+          mix_dma(ty, m, mrs, ty == 0 ? vb0 : ty == 1 ? vb1 : ty == 2 ? kb : eb);
+        }
+        constexpr int rv = MS::read(ps_);
+        if constexpr (rv >= 0) {
+          constexpr int ty = rv / 8, m = rv % 8;
+          if constexpr (ty < 2) mrs = mix_slot(10 + m, q, sring_v);
+          else mrs = mix_slot(ty == 2 ? m : 5 + m, q + 2, sring);
+        }
+      } else {
+        if constexpr (SC::row_dma(ps_) >= 0) {
+          constexpr int k = SC::row_dma(ps_);
+          if (dmas) row_dma(k, rs[k % 2], stw);
+        }
+        if constexpr (SC::row_read(ps_) >= 0) {
+          constexpr int k = SC::row_read(ps_);
+          if constexpr (DM != 0) rs[k % 2] = row_slot(k, q + 2, sring);
+        }
       }
       // 4. fragment loads, address moves
       if constexpr (SC::kload(i) >= 0) kload(SC::kload(i) % 9);
+      if constexpr (MIX) {  // e8m0: steps 0..7 of the next tile once its QK is past them, step 8 after
+        if constexpr (i == 20) scload_lo();
+        if constexpr (i == 22) scload_hi();
+        if constexpr (i == 1) scload_8();
+      }
       if constexpr (SC::vload(i) >= 0) {
         constexpr int g = SC::vload(i);
         if constexpr (g < 8) vload(H, g);
         else vload(IT, 0);  // group 0 of the next iteration (half IT ^ 1 ^ 1)
       }
       if constexpr (i == SC::kRebaseK) {
-        const int dk = IT == 0 ? C::TSTAGE : (((q + 1) & 3) - (q & 3)) * C::PSTAGE - C::TSTAGE;
+        if constexpr (MIX) {  // K and e8m0 tiles: + 32 rows, or on to the next pair's stage
+          const int step = (q % 3 == 2) ? -2 : 1;
+          const int dk = IT == 0 ? 32 * M128::KST : step * M128::KSTAGE - 32 * M128::KST;
+          const int ds = IT == 0 ? 2048 : step * M128::SSTAGE - 2048;
+          const int d8 = IT == 0 ? 128 : step * M128::SSTAGE - 128;
+          ka[0] += dk;
+          ka[1] += ds;
+          ka[2] += d8;
 #pragma unroll
-        for (int jj = 0; jj < 6; ++jj) {
-          ka[jj] += dk;
-          asm volatile("" : "+v"(ka[jj]));
+          for (int jj = 0; jj < 3; ++jj) asm volatile("" : "+v"(ka[jj]));
+        } else {
+          const int dk = IT == 0 ? G128::TSTAGE : (((q + 1) & 3) - (q & 3)) * G128::PSTAGE - G128::TSTAGE;
+#pragma unroll
+          for (int jj = 0; jj < 6; ++jj) {
+            ka[jj] += dk;
+            asm volatile("" : "+v"(ka[jj]));
+          }
         }
       }
-      if constexpr (IT == 0 && i == SC::kRebaseV) {  // pair q - 2 -> q - 1
-        const int dv = (((q - 1) & 3) - ((q - 2) & 3)) * C::PSTAGE;
+      if constexpr (MIX && i == SC::kRebaseV) {  // half stage (t + 1) & 3 -> (t + 2) & 3
+        const int dv = (IT == 0 && (q & 1)) ? -3 * M128::VSTAGE : M128::VSTAGE;
+        va[0] += dv;
+        asm volatile("" : "+v"(va[0]));
+      }
+      if constexpr (!MIX && IT == 0 && i == SC::kRebaseV) {  // pair q - 2 -> q - 1
+        const int dv = (((q - 1) & 3) - ((q - 2) & 3)) * G128::PSTAGE;
 #pragma unroll
         for (int jj = 0; jj < 8; ++jj) {
           va[jj] += dv;
@@ -606,21 +906,35 @@ __global__ __launch_bounds__(256, 1) void decode_h128f_kernel(const DecodeParams
       }
       lds_barrier();
       issue_slots(2);
-      issue_rows(0);
+      if constexpr (MIX) mix_issue_ks(0);
+      else issue_rows(0);
       issue_slots(3);
-      issue_rows(1);
-      if (first) {  // this wave's Q rows landed (issued before the 20 or 22 DMAs since)
-        if (w == 0) wait_vmcnt<IDX ? 2 * C::DMAX + 2 : 2 * C::DMAX>();
-        else if (w == 1) wait_vmcnt<2 * C::DMAX>();
-        else wait_vmcnt<2 * C::DMAX - 2>();
+      if constexpr (MIX) mix_issue_ks(1);
+      else issue_rows(1);
+      // two-cache mode: K and e8m0 windows of a pair per wave, 5 + 5, 5 + 5, 5 + 4, 4 + 4
+      constexpr int S0 = IDX ? 1 : 0;
+      if (first) {  // this wave's Q rows landed (issued before the DMAs since)
+        if constexpr (MIX) {
+          wait_vmcnt_w<2 * S0 + 20, 20, 18, 16>(w);
+        } else {
+          if (w == 0) wait_vmcnt<IDX ? 2 * G128::DMAX + 2 : 2 * G128::DMAX>();
+          else if (w == 1) wait_vmcnt<2 * G128::DMAX>();
+          else wait_vmcnt<2 * G128::DMAX - 2>();
+        }
         read_q();
       }
-      wait_rows();
-      lds_barrier();  // pair 0 visible; every wave's Q^T reads done (stage 2 reusable)
+      if constexpr (MIX) wait_vmcnt_w<S0 + 10, 10, 9, 8>(w);  // K and e8m0 of pair 0
+      else wait_rows();
+      lds_barrier();  // pair 0 visible; every wave's Q^T reads done (its stages reusable)
       init_ka();
       init_va();
       kload(0);
       kload(1);
+      if constexpr (MIX) {
+        scload_lo();
+        scload_hi();
+        scload_8();
+      }
       vload(1, 0);
       // pairs: the first two (pipeline fill), the steady ones (every part of
       // both iterations runs: PV pairs q - 2 >= 0 and q - 1, QK tiles 2q + 1 < n),
@@ -690,9 +1004,17 @@ __global__ __launch_bounds__(256, 1) void decode_h128f_kernel(const DecodeParams
 
 hipError_t launch_decode_h128f(const DecodeParams& p, int grid, hipStream_t stream) {
   if (p.kv_indices != nullptr)
-    hipLaunchKernelGGL(decode_h128f_kernel<true>, dim3(grid), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((decode_h128_kernel<true, false>), dim3(grid), dim3(256), 0, stream, p);
   else
-    hipLaunchKernelGGL(decode_h128f_kernel<false>, dim3(grid), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((decode_h128_kernel<false, false>), dim3(grid), dim3(256), 0, stream, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_decode_h128m(const DecodeParams& p, int grid, hipStream_t stream) {
+  if (p.kv_indices != nullptr)
+    hipLaunchKernelGGL((decode_h128_kernel<true, true>), dim3(grid), dim3(256), 0, stream, p);
+  else
+    hipLaunchKernelGGL((decode_h128_kernel<false, true>), dim3(grid), dim3(256), 0, stream, p);
   return hipGetLastError();
 }
 

@@ -61,6 +61,7 @@ hipError_t launch_decode(const DecodeParams& p, int kv_mode, int grid, hipStream
 hipError_t launch_combine(const DecodeParams& p, hipStream_t stream);
 // decode_h128.hip: H = 128 with the fp8 cache
 hipError_t launch_decode_h128f(const DecodeParams& p, int grid, hipStream_t stream);
+hipError_t launch_decode_h128m(const DecodeParams& p, int grid, hipStream_t stream);
 
 // neighbours.hip
 hipError_t launch_absorb_q(const uint16_t* q_nope, const uint16_t* q_rope, const uint16_t* w_uk, int batch,

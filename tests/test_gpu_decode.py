@@ -121,7 +121,7 @@ def test_mxfp4_scale_row_stride(cuda, heads, mode):
         assert torch.equal(got, base), cols
 
 
-@pytest.mark.parametrize("heads,mode", [(16, "fp8"), (128, "fp8"), (16, "mxfp4")])
+@pytest.mark.parametrize("heads,mode", [(16, "fp8"), (128, "fp8"), (16, "mxfp4"), (128, "mxfp4k_fp8v")])
 def test_cache_permutation_is_exact(cuda, heads, mode):
     # moving cache rows together with kv_indices leaves the output bit-identical
     print(f"permutation H={heads} mode={mode}", flush=True)
