@@ -56,13 +56,6 @@ __device__ __forceinline__ uint32_t cvt_fp4_byte(uint32_t word, float scale) {
   return __builtin_bit_cast(uint32_t, r);
 }
 
-// two floats -> bf16 pair (RNE, v_cvt_pk_bf16_f32), a in the low half
-__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
-  typedef __bf16 v2bf_t __attribute__((ext_vector_type(2)));
-  const v2bf_t r = {(__bf16)a, (__bf16)b};
-  return __builtin_bit_cast(uint32_t, r);
-}
-
 __device__ __forceinline__ float e8m0_to_f32(uint32_t e) {
   return e == 0 ? __uint_as_float(0x00400000u) : __uint_as_float(e << 23);
 }
@@ -731,8 +724,8 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
       const int d = 128 * w + 16 * dt + 4 * g;
-      const uint32_t lo = f32_to_bf16_bits(o[dt][0] * inv) | (f32_to_bf16_bits(o[dt][1] * inv) << 16);
-      const uint32_t hi = f32_to_bf16_bits(o[dt][2] * inv) | (f32_to_bf16_bits(o[dt][3] * inv) << 16);
+      const uint32_t lo = pack_bf16x2(o[dt][0] * inv, o[dt][1] * inv);
+      const uint32_t hi = pack_bf16x2(o[dt][2] * inv, o[dt][3] * inv);
       *reinterpret_cast<uint2*>(orow + d) = make_uint2(lo, hi);
     }
   } else {
@@ -740,8 +733,8 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
       const int d = 128 * w + 16 * dt + 4 * g;
-      const uint32_t lo = f32_to_bf16_bits(o[dt][0] * inv) | (f32_to_bf16_bits(o[dt][1] * inv) << 16);
-      const uint32_t hi = f32_to_bf16_bits(o[dt][2] * inv) | (f32_to_bf16_bits(o[dt][3] * inv) << 16);
+      const uint32_t lo = pack_bf16x2(o[dt][0] * inv, o[dt][1] * inv);
+      const uint32_t hi = pack_bf16x2(o[dt][2] * inv, o[dt][3] * inv);
       *reinterpret_cast<uint2*>(prow + d) = make_uint2(lo, hi);
     }
     if (w == 0 && g == 0) p.part_lse[(int64_t)slot * 16 + head] = L > 0.f ? m_ref + __log2f(L) : neg_inf();
@@ -804,7 +797,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const DecodeParams p) {
   uint32_t w4[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
-    w4[i] = f32_to_bf16_bits(acc[2 * i] * inv) | (f32_to_bf16_bits(acc[2 * i + 1] * inv) << 16);
+    w4[i] = pack_bf16x2(acc[2 * i] * inv, acc[2 * i + 1] * inv);
   *reinterpret_cast<uint4*>(p.out + ((int64_t)b * H + head) * kVDim + d0) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
 }
 

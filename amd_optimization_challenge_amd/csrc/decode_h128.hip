@@ -138,28 +138,30 @@ __device__ __forceinline__ void wait_vmcnt_w(int w) {
 // the builtin would give every MFMA of the kernel an AGPR accumulator).  All
 // MFMAs are issued by asm so that each keeps its place in the source order
 // (the builtins are pure values the compiler may move past the MFMAs they are
-// meant to interleave with).  The compiler does not see these MFMAs, so each is
-// fenced with s_nop (VALU writes of its sources before, source reads after),
-// and a result is read by VALU only after a drain (32 wait states; a VALU read
-// of a 16-pass XDL result needs 19).  A dependent chain on one accumulator
-// needs no wait states.
+// meant to interleave with).  The compiler does not see these MFMAs, so the
+// schedule provides their wait states: no VALU writes an MFMA operand within
+// the 2 wait states before it (the fragments come from LDS, P' and its scales
+// are built slots earlier), a result is read by VALU only 19 or more after it
+// (16-pass XDL), no VALU touches an accumulator in flight, and a dependent
+// chain on one accumulator needs none.  tests/test_mfma_hazards.py checks the
+// built code object for both rules along every path.
 __device__ __forceinline__ void qk_first(v16f& d, const v8i& a, const v8i& b) {
-  asm volatile("s_nop 1\n\tv_mfma_f32_32x32x64_f8f6f4 %0, %1, %2, 0\n\ts_nop 2" : "=&v"(d) : "v"(a), "v"(b));
+  asm volatile("v_mfma_f32_32x32x64_f8f6f4 %0, %1, %2, 0" : "=&v"(d) : "v"(a), "v"(b));
 }
 __device__ __forceinline__ void qk_acc(v16f& d, const v8i& a, const v8i& b) {
-  asm volatile("s_nop 1\n\tv_mfma_f32_32x32x64_f8f6f4 %0, %1, %2, %0\n\ts_nop 2" : "+v"(d) : "v"(a), "v"(b));
+  asm volatile("v_mfma_f32_32x32x64_f8f6f4 %0, %1, %2, %0" : "+v"(d) : "v"(a), "v"(b));
 }
 // the same with fp4 A (4 VGPRs: 32 e2m1 values) at the lane's e8m0 scale sa
 // (byte 0), fp8 B at unit scale
 __device__ __forceinline__ void qk4_first(v16f& d, const v4i& a, const v8i& b, int sa) {
   asm volatile(
-      "s_nop 1\n\tv_mfma_scale_f32_32x32x64_f8f6f4 %0, %1, %2, 0, %3, %4 op_sel_hi:[0,0,0] cbsz:4\n\ts_nop 2"
+      "v_mfma_scale_f32_32x32x64_f8f6f4 %0, %1, %2, 0, %3, %4 op_sel_hi:[0,0,0] cbsz:4"
       : "=&v"(d)
       : "v"(a), "v"(b), "v"(sa), "v"(127));
 }
 __device__ __forceinline__ void qk4_acc(v16f& d, const v4i& a, const v8i& b, int sa) {
   asm volatile(
-      "s_nop 1\n\tv_mfma_scale_f32_32x32x64_f8f6f4 %0, %1, %2, %0, %3, %4 op_sel_hi:[0,0,0] cbsz:4\n\ts_nop 2"
+      "v_mfma_scale_f32_32x32x64_f8f6f4 %0, %1, %2, %0, %3, %4 op_sel_hi:[0,0,0] cbsz:4"
       : "+v"(d)
       : "v"(a), "v"(b), "v"(sa), "v"(127));
 }
@@ -167,7 +169,7 @@ __device__ __forceinline__ void drain_v(v16f& x) { asm volatile("s_nop 15\n\ts_n
 // PV: O^T += V^T . P'^T with an e8m0 scale on B (one per lane: its head), A at
 // unit scale; accumulator in AGPRs
 __device__ __forceinline__ void pv_mfma(v16f& acc, const v8i& a, const v8i& b, int bscale) {
-  asm volatile("s_nop 1\n\tv_mfma_scale_f32_32x32x64_f8f6f4 %0, %1, %2, %0, %3, %4 op_sel_hi:[0,0,0]"
+  asm volatile("v_mfma_scale_f32_32x32x64_f8f6f4 %0, %1, %2, %0, %3, %4 op_sel_hi:[0,0,0]"
                : "+a"(acc)
                : "v"(a), "v"(b), "v"(127), "v"(bscale));
 }
@@ -427,22 +429,22 @@ __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams 
   // sbase) and its DMA into the pair's stage (stage_w: the stage plus 1 KiB w;
   // window k lands 4 KiB k further).  k is a compile-time constant at every
   // call: the map register and its half are fixed.
+  // (each use first marks its map register as rewritten, which costs no
+  // instruction, so that no decode is hoisted out of the loop and kept live)
   auto row_slot = [&](int k, int rq, uint32_t sbase) __attribute__((always_inline)) -> int {
-    uint32_t d = dmap[k / 2];
-    asm volatile("" : "+v"(d));  // opaque map: its decode is not hoisted out of the loop
-    const uint32_t e = (d >> (16 * (k % 2))) & 0xFFFFu;
+    asm volatile("" : "+v"(dmap[k / 2]));
+    const uint32_t r = (dmap[k / 2] >> (10 + 16 * (k % 2))) & 63u;
     if constexpr (IDX) {
       typedef __attribute__((address_space(3))) int lds_int;
-      return *(const lds_int*)(uintptr_t)(sbase + ((e >> 8) & 0xFCu));  // 4r: entry r of the ring stage
+      return *(const lds_int*)(uintptr_t)(sbase + 4 * r);  // entry r of the ring stage
     } else {
-      return min(t_beg + 64 * rq + (int)(e >> 10), t_end - 1);
+      return min(t_beg + 64 * rq + (int)r, t_end - 1);
     }
   };
   auto row_dma = [&](int k, int sl, uint32_t stage_w) __attribute__((always_inline)) {
     if (k < G128::DMAX - 1 || w < 2) {
-      uint32_t d = dmap[k / 2];
-      asm volatile("" : "+v"(d));
-      const uint32_t off = (d >> (16 * (k % 2))) & 1023u;
+      asm volatile("" : "+v"(dmap[k / 2]));
+      const uint32_t off = (dmap[k / 2] >> (16 * (k % 2))) & 1023u;
       const uint8_t* src = p.k_cache + ((uint64_t)(uint32_t)sl * (uint32_t)p.k_row_stride + off);
       asm volatile("s_add_u32 m0, %0, %1\n\tglobal_load_lds_dwordx4 %2, off"
                    :
@@ -480,14 +482,13 @@ __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams 
   };
   // two-cache mode: the slot of map entry k's row in pair pq (ring stage sbase)
   auto mix_slot = [&](int k, int pq, uint32_t sbase) __attribute__((always_inline)) -> int {
-    uint32_t d = dmap[k / 2];
-    asm volatile("" : "+v"(d));
-    const uint32_t e = (d >> (16 * (k % 2))) & 0xFFFFu;
+    asm volatile("" : "+v"(dmap[k / 2]));
+    const uint32_t r = (dmap[k / 2] >> (9 + 16 * (k % 2))) & 63u;
     if constexpr (IDX) {
       typedef __attribute__((address_space(3))) int lds_int;
-      return *(const lds_int*)(uintptr_t)(sbase + ((e >> 7) & ~3u));  // 4r
+      return *(const lds_int*)(uintptr_t)(sbase + 4 * r);
     } else {
-      return min(t_beg + 64 * pq + (int)(e >> 9), t_end - 1);
+      return min(t_beg + 64 * pq + (int)r, t_end - 1);
     }
   };
   // window m of type ty (0, 1: V half; 2: K; 3: e8m0) from slot sl into the
@@ -495,9 +496,8 @@ __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams 
   auto mix_dma = [&](int ty, int m, int sl, uint32_t base) __attribute__((always_inline)) {
     if (MS::has(ty, m, w)) {
       const int k = ty < 2 ? 10 + m : ty == 2 ? m : 5 + m;
-      uint32_t d = dmap[k / 2];
-      asm volatile("" : "+v"(d));
-      const uint32_t off = (d >> (16 * (k % 2))) & 511u;
+      asm volatile("" : "+v"(dmap[k / 2]));
+      const uint32_t off = (dmap[k / 2] >> (16 * (k % 2))) & 511u;
       if (ty == 3) {
         const uint8_t* src = p.k_scales + ((uint64_t)(uint32_t)sl * (uint32_t)p.k_scale_stride + off);
         asm volatile("s_add_u32 m0, %0, %1\n\tglobal_load_lds_ubyte %2, off"
@@ -663,7 +663,10 @@ __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams 
     constexpr int u = decltype(U)::value;
     constexpr int k = decltype(K)::value;
     if constexpr (k == 0) {
-      asm volatile("s_nop 15" : "+v"(s));  // the tile's last QK MFMA (two slots back) has retired
+      // the tile's last QK MFMA issued two slots back: slots 0 and 1 hold at
+      // least 13 instructions (MFMAs, fragment loads), and these 7 complete the
+      // 19 a VALU read of its result needs, with one to spare
+      asm volatile("s_nop 6" : "+v"(s));
       const int nval = ntok - C::HT * t;
       if (nval < C::HT) {  // token 8(r >> 2) + (r & 3) (+ 4hh) >= nval: a constant vs the lane limit
         const int lim = nval - 4 * hh;
@@ -701,12 +704,12 @@ __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams 
     } else {  // steps 14..21: quad qd, hi term then lo term (the hi codes decoded again)
       constexpr int qd = (k - 14) / 2;
       if constexpr ((k - 14) % 2 == 0) {
-        bh[4 * u + qd] = (int)pack4_fp8(s[4 * qd], s[4 * qd + 1], s[4 * qd + 2], s[4 * qd + 3]);
+        bh[4 * u + qd] = (int)pack4_fp8_over((uint32_t)bh[4 * u + qd], s[4 * qd], s[4 * qd + 1], s[4 * qd + 2], s[4 * qd + 3]);
       } else {
         const v2f h01 = __builtin_amdgcn_cvt_pk_f32_fp8(bh[4 * u + qd], false);
         const v2f h23 = __builtin_amdgcn_cvt_pk_f32_fp8(bh[4 * u + qd], true);
-        bl[4 * u + qd] = (int)pack4_fp8(s[4 * qd] - h01[0], s[4 * qd + 1] - h01[1], s[4 * qd + 2] - h23[0],
-                                          s[4 * qd + 3] - h23[1]);
+        bl[4 * u + qd] = (int)pack4_fp8_over((uint32_t)bl[4 * u + qd], s[4 * qd] - h01[0], s[4 * qd + 1] - h01[1],
+                                               s[4 * qd + 2] - h23[0], s[4 * qd + 3] - h23[1]);
       }
     }
   };
@@ -977,8 +980,8 @@ __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams 
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int d = 32 * dt + 8 * q + 4 * hh;
-      const uint32_t lo = f32_to_bf16_bits(o[dt][4 * q] * inv) | (f32_to_bf16_bits(o[dt][4 * q + 1] * inv) << 16);
-      const uint32_t hi = f32_to_bf16_bits(o[dt][4 * q + 2] * inv) | (f32_to_bf16_bits(o[dt][4 * q + 3] * inv) << 16);
+      const uint32_t lo = pack_bf16x2(o[dt][4 * q] * inv, o[dt][4 * q + 1] * inv);
+      const uint32_t hi = pack_bf16x2(o[dt][4 * q + 2] * inv, o[dt][4 * q + 3] * inv);
       *reinterpret_cast<uint2*>(ob + l32 * ORST + 2 * d) = make_uint2(lo, hi);
     }
   }

@@ -77,6 +77,13 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
   return u >> 16;
 }
 
+// two floats -> bf16 pair (RNE, v_cvt_pk_bf16_f32), a in the low half
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  typedef __bf16 v2bf_t __attribute__((ext_vector_type(2)));
+  const v2bf_t r = {(__bf16)a, (__bf16)b};
+  return __builtin_bit_cast(uint32_t, r);
+}
+
 // Round-to-nearest-even f32 -> OCP e4m3fn code for |f| <= 448.
 __device__ __forceinline__ uint32_t f32_to_e4m3fn(float f) {
   uint32_t u = __float_as_uint(f);
@@ -174,6 +181,13 @@ __device__ __forceinline__ v4f mfma16x32_bf16(v8bf a, v8bf b, v4f c) {
 // Pack four floats (each in [0, 448]) into four e4m3fn bytes, element i in byte i.
 __device__ __forceinline__ uint32_t pack4_fp8(float a, float b, float c, float d) {
   int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+  return (uint32_t)w;
+}
+// the same written over `old` (whose bytes all end replaced): the converts
+// can then reuse old's register instead of a zeroed copy
+__device__ __forceinline__ uint32_t pack4_fp8_over(uint32_t old, float a, float b, float c, float d) {
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, (int)old, false);
   w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
   return (uint32_t)w;
 }

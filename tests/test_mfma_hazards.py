@@ -1,0 +1,185 @@
+"""Wait-state hazards of the hand-written MFMAs of the H = 128 kernels.
+
+decode_h128.hip issues its MFMAs by inline asm (each must keep its slot of the
+static schedule), so the compiler's hazard recognizer does not see them and
+the kernel must provide their wait states itself.  This test reads the
+gfx950 code object of the built decode_h128.o (llvm-objdump of our own
+build) and checks, along every control-flow path (branch targets included):
+
+* a VALU write of a VGPR that an MFMA reads (A, B, C or scale operand) is at
+  least 2 wait states before the MFMA;
+* an MFMA's result registers are neither read nor written by a VALU, LDS or
+  memory instruction within 20 wait states after it (a VALU read of a 16-pass
+  XDL result needs 19), except by the next MFMA of a same-shape accumulate
+  chain on those registers.
+
+s_nop N counts N + 1 wait states, every other instruction one.
+"""
+import os
+import re
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+OBJ = os.path.join(ROOT, "amd_optimization_challenge_amd", "_build", "decode_h128.o")
+LLVM = "/opt/rocm/llvm/bin"
+PRE_WS, POST_WS = 2, 20
+
+INSN = re.compile(r"^\s+(\S+)\s*(.*?)\s*//\s*([0-9A-Fa-f]+):(.*)$")
+TARGET = re.compile(r"<(\S+?)(?:\+0x([0-9a-f]+))?>")
+FUNC = re.compile(r"^([0-9a-f]+) <(\S+)>:$")
+REG = re.compile(r"\b([va])(?:\[(\d+):(\d+)\]|(\d+)(?!\d))")
+
+
+def regs(text):
+    out = set()
+    for m in REG.finditer(text):
+        if m.group(4) is not None:
+            out.add((m.group(1), int(m.group(4))))
+        else:
+            out |= {(m.group(1), i) for i in range(int(m.group(2)), int(m.group(3)) + 1)}
+    return out
+
+
+def operands(args):
+    args = re.split(r"\s(?:op_sel|op_sel_hi|cbsz|abid|blgp|offset|glc|slc|nt|sc0|sc1)\b", args)[0]
+    return [a.strip() for a in args.split(",") if a.strip()]
+
+
+def disassemble(obj, tmp):
+    fat = os.path.join(tmp, "fat.bin")
+    co = os.path.join(tmp, "dev.co")
+    subprocess.run([f"{LLVM}/llvm-objcopy", f"--dump-section=.hip_fatbin={fat}", obj, os.path.join(tmp, "host.o")],
+                   check=True, capture_output=True)
+    subprocess.run([f"{LLVM}/clang-offload-bundler", "--type=o", "--targets=hipv4-amdgcn-amd-amdhsa--gfx950",
+                    f"--input={fat}", f"--output={co}", "--unbundle"], check=True, capture_output=True)
+    res = subprocess.run([f"{LLVM}/llvm-objdump", "-d", "--mcpu=gfx950", co], check=True, capture_output=True,
+                         text=True)
+    return res.stdout
+
+
+def parse(text):
+    """{function: [(addr, mnemonic, args, target_addr or None)]}"""
+    funcs, cur, base = {}, None, {}
+    for line in text.splitlines():
+        m = FUNC.match(line)
+        if m:
+            cur = m.group(2)
+            base[cur] = int(m.group(1), 16)
+            funcs[cur] = []
+            continue
+        m = INSN.match(line)
+        if m and cur:
+            mnem, args, addr, tail = m.group(1), m.group(2), int(m.group(3), 16), m.group(4)
+            tgt = None
+            if mnem.startswith("s_branch") or mnem.startswith("s_cbranch"):
+                t = TARGET.search(tail)
+                if t and t.group(1) in base:
+                    tgt = base[t.group(1)] + int(t.group(2) or "0", 16)
+            funcs[cur].append((addr, mnem, args, tgt))
+    return funcs
+
+
+def wait_states(mnem, args):
+    if mnem == "s_nop":
+        return int(args.split()[0], 0) + 1
+    return 1
+
+
+def check_function(insns):
+    idx = {a: i for i, (a, _, _, _) in enumerate(insns)}
+    preds = {i: [] for i in range(len(insns))}
+    succs = {i: [] for i in range(len(insns))}
+    for i, (_, mnem, _, tgt) in enumerate(insns):
+        falls = not (mnem == "s_branch" or mnem.startswith("s_endpgm") or mnem.startswith("s_setpc"))
+        if falls and i + 1 < len(insns):
+            preds[i + 1].append(i)
+            succs[i].append(i + 1)
+        if tgt is not None and tgt in idx:
+            preds[idx[tgt]].append(i)
+            succs[i].append(idx[tgt])
+    bad = []
+    for i, (_, mnem, args, _) in enumerate(insns):
+        if not mnem.startswith("v_mfma"):
+            continue
+        ops = operands(args)
+        dst = regs(ops[0])
+        src = set()
+        for o in ops[1:]:
+            src |= regs(o)
+        # (1) VALU writes of the sources within PRE_WS wait states before
+        stack = [(p, 0) for p in preds[i]]
+        seen = set()
+        while stack:
+            j, ws = stack.pop()
+            if ws >= PRE_WS or (j, ws) in seen:
+                continue
+            seen.add((j, ws))
+            m2, a2 = insns[j][1], insns[j][2]
+            if m2.startswith("v_") and not m2.startswith("v_mfma"):
+                o2 = operands(a2)
+                # (a swap writes both of its operands)
+                written = regs(a2) if "swap" in m2 else (regs(o2[0]) if o2 else set())
+                if written & src:
+                    bad.append(f"VALU write {m2} {a2} {PRE_WS - ws} wait states before {mnem} {args}")
+            stack += [(p, ws + wait_states(m2, a2)) for p in preds[j]]
+        # (2) any access to the results within POST_WS wait states after
+        stack = [(s, 0) for s in succs[i]]
+        seen = set()
+        while stack:
+            j, ws = stack.pop()
+            if ws >= POST_WS or (j, ws) in seen:
+                continue
+            seen.add((j, ws))
+            m2, a2 = insns[j][1], insns[j][2]
+            touched = regs(a2)
+            if m2.startswith("v_mfma"):
+                o2 = operands(a2)
+                same_chain = m2 == mnem and o2 and regs(o2[0]) == dst and len(o2) > 3 and regs(o2[3]) == dst
+                if (touched & dst) and not same_chain:
+                    bad.append(f"{m2} {a2} touches the result of {mnem} {args} after {ws} wait states")
+            elif touched & dst and (m2.startswith("v_") or m2.startswith("ds_") or m2.startswith("global_")
+                                     or m2.startswith("buffer_") or m2.startswith("scratch_")):
+                bad.append(f"{m2} {a2} touches the result of {mnem} {args} after {ws} wait states")
+            stack += [(s, ws + wait_states(m2, a2)) for s in succs[j]]
+    return bad
+
+
+def test_hand_written_mfma_hazards(tmp_path):
+    if not os.path.exists(OBJ):
+        pytest.skip("decode_h128.o not built (run __graft_entry__.build())")
+    if not all(os.path.exists(f"{LLVM}/{t}") for t in ("llvm-objcopy", "clang-offload-bundler", "llvm-objdump")):
+        pytest.skip("ROCm LLVM tools not found")
+    funcs = parse(disassemble(OBJ, str(tmp_path)))
+    kernels = {k: v for k, v in funcs.items() if "decode_h128_kernel" in k}
+    assert len(kernels) == 4, sorted(funcs)
+    report = []
+    for name, insns in kernels.items():
+        n_mfma = sum(1 for _, m, _, _ in insns if m.startswith("v_mfma"))
+        assert n_mfma >= 50, (name, n_mfma)
+        report += [f"{name}: {b}" for b in check_function(insns)]
+    assert not report, "\n".join(report[:20])
+
+
+def test_checker_flags_planted_hazards():
+    """The checker itself: a VALU write one wait state before an MFMA source
+    read, and a VALU read of an MFMA result 5 wait states after it, are caught;
+    the same code with enough s_nop passes."""
+    def prog(lines):
+        return [(4 * i, m, a, None) for i, (m, a) in enumerate(lines)]
+    mf = ("v_mfma_f32_32x32x64_f8f6f4", "v[0:15], v[16:23], v[24:31], v[0:15]")
+    assert check_function(prog([("v_mov_b32_e32", "v20, v40"), mf, ("s_nop", "15"), ("s_nop", "4")]))
+    assert not check_function(prog([("v_mov_b32_e32", "v20, v40"), ("s_nop", "1"), mf, ("s_nop", "15"),
+                                    ("s_nop", "4")]))
+    assert check_function(prog([("s_nop", "1"), mf, ("s_nop", "3"), ("v_add_f32_e32", "v40, v3, v41")]))
+    assert not check_function(prog([("s_nop", "1"), mf, ("s_nop", "15"), ("s_nop", "3"),
+                                    ("v_add_f32_e32", "v40, v3, v41")]))
+    # an accumulate chain on the same registers needs no wait states
+    assert not check_function(prog([("s_nop", "1"), mf, mf, ("s_nop", "15"), ("s_nop", "4")]))
+    # a branch back to the MFMA brings the loop's tail into its window
+    loop = [("s_nop", "1"), mf, ("s_nop", "15"), ("s_nop", "4"), ("v_mov_b32_e32", "v17, v40"),
+            ("s_cbranch_scc1", "")]
+    p = prog(loop)
+    p[-1] = (p[-1][0], "s_cbranch_scc1", "", 4)
+    assert check_function(p)
