@@ -740,6 +740,9 @@ __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams 
     constexpr int DM = decltype(dm_tag)::value;
     asm volatile("" : "+s"(q));  // nothing that depends on q is precomputed (and kept live) outside the pair
     const bool dmas = DM == 1 || (DM == 2 && q + 2 < npair);
+    // two-cache mode: a pair past the item's last (draining the pipeline)
+    // issues no DMAs, and its barriers wait for every DMA still in flight
+    const bool live = !GUARD || q < npair;
     uint32_t stw = 0, sring = 0, sring_v = 0, kb = 0, eb = 0, vb0 = 0, vb1 = 0;
     if constexpr (MIX) {  // K and e8m0 of pair q + 2, V halves of pair q
       sring = sring_of(q + 2);
@@ -752,7 +755,7 @@ __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams 
       stw = stage_of(q + 2);
       sring = sring_of(q + 2);
     }
-    static_for<0, 2 * SC::kSlots>([&](auto S) __attribute__((always_inline)) {
+    auto slot = [&](auto S) __attribute__((always_inline)) {
       constexpr int ps_ = decltype(S)::value;  // slot of the pair
       constexpr int IT = ps_ / SC::kSlots;      // iteration of the pair (tile t = 2q + IT)
       constexpr int i = ps_ % SC::kSlots;       // slot of the iteration
@@ -787,12 +790,16 @@ __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams 
       // 2. barriers: pair q - 2's stage free (every wave's last V^T read of it
       // done); pair q + 1 published (its rows landed)
       if constexpr (ps_ == SC::kStageFree) {
-        if constexpr (MIX) mix_wait_free();  // and V(q - 1) half 0 published
+        if constexpr (MIX) {  // and V(q - 1) half 0 published
+          if (live) mix_wait_free();
+          else wait_vmcnt<0>();
+        }
         lds_barrier();
       }
       if constexpr (ps_ == SC::kBarrier) {
         if constexpr (MIX) {
-          mix_wait_pub();
+          if (live) mix_wait_pub();
+          else wait_vmcnt<0>();
         } else if constexpr (DM == 1) {
           wait_rows();
         } else if constexpr (DM == 0) {
@@ -805,17 +812,19 @@ __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams 
       }
       // 3. slot indices of pair q + 4, rows of pair q + 2
       if constexpr (ps_ == SC::kSlotDma) issue_slots(q + 4);
-      if constexpr (MIX) {  // every DMA of the pair, always (uniform vmcnt counts)
+      if constexpr (MIX) {  // every DMA of a live pair (uniform vmcnt counts)
         constexpr int ev = MS::dma(ps_);
         if constexpr (ev >= 0) {
           constexpr int ty = ev / 8, m = ev % 8;
-          mix_dma(ty, m, mrs, ty == 0 ? vb0 : ty == 1 ? vb1 : ty == 2 ? kb : eb);
+          if (live) mix_dma(ty, m, mrs, ty == 0 ? vb0 : ty == 1 ? vb1 : ty == 2 ? kb : eb);
         }
         constexpr int rv = MS::read(ps_);
         if constexpr (rv >= 0) {
           constexpr int ty = rv / 8, m = rv % 8;
-          if constexpr (ty < 2) mrs = mix_slot(10 + m, q, sring_v);
-          else mrs = mix_slot(ty == 2 ? m : 5 + m, q + 2, sring);
+          if (live) {
+            if constexpr (ty < 2) mrs = mix_slot(10 + m, q, sring_v);
+            else mrs = mix_slot(ty == 2 ? m : 5 + m, q + 2, sring);
+          }
         }
       } else {
         if constexpr (SC::row_dma(ps_) >= 0) {
@@ -886,7 +895,10 @@ __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams 
         }
       }
       __builtin_amdgcn_sched_barrier(0);
-    });
+    };
+    static_for<0, SC::kSlots>(slot);
+    // the last pair's second iteration has no work (no QK, softmax or PV tile)
+    if (!GUARD || q <= npair) static_for<SC::kSlots, 2 * SC::kSlots>(slot);
   };
   const std::true_type Y{};
   const std::false_type N{};
@@ -966,6 +978,8 @@ __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams 
   }
 
   // ---- finish: normalize, transpose O^T through LDS, coalesced row stores ------
+  // (16-byte stores of whole row segments: 8-byte stores straight from the
+  // accumulators touch 32 rows per instruction and issue far slower)
   asm volatile("s_nop 15\n\ts_nop 15" ::: "memory");  // last PV MFMAs retired before O^T is read
   const float L = xhalf_sum(l_run);
   const float inv = L > 0.f ? vscale / L : 0.f;
