@@ -86,12 +86,15 @@ static int blocks_per_cu(int num_heads, int kv_mode) {
   return (kv_mode == MLA_KV_FP8 || kv_mode == MLA_KV_MXFP4 || kv_mode < 0) ? 2 : 1;
 }
 
-// Items the planner aims for: one per resident work-group slot, raised to two
-// per sequence when the batch is large so long sequences still get split,
-// capped at four rounds of slots.
+// Items the planner aims for: one per resident work-group slot while the
+// batch is smaller than the slots; once it fills them, 1.5 per slot (or one
+// per sequence, if more), so that long sequences are still split and the
+// items balance without splitting every sequence (each split costs a second
+// prologue and a partial output); capped at four rounds of slots.
 int target_items_for(int batch, int num_heads, int kv_mode, int num_cu) {
   const int slots = num_cu * blocks_per_cu(num_heads, kv_mode);
-  int t = 2 * batch > slots ? 2 * batch : slots;
+  if (batch < slots) return slots;
+  const int t = batch > slots * 3 / 2 ? batch : slots * 3 / 2;
   return t < 4 * slots ? t : 4 * slots;
 }
 

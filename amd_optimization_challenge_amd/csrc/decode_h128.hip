@@ -446,10 +446,12 @@ __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams 
       asm volatile("" : "+v"(dmap[k / 2]));
       const uint32_t off = (dmap[k / 2] >> (16 * (k % 2))) & 1023u;
       const uint8_t* src = p.k_cache + ((uint64_t)(uint32_t)sl * (uint32_t)p.k_row_stride + off);
-      asm volatile("s_add_u32 m0, %0, %1\n\tglobal_load_lds_dwordx4 %2, off"
-                   :
+      uint32_t saved;  // M0 saved and restored, one wait state before the DMA (see dma16_to_lds)
+      asm volatile("s_mov_b32 %0, m0\n\ts_add_u32 m0, %1, %2\n\ts_mov_b32 %0, %0\n\t"
+                   "global_load_lds_dwordx4 %3, off\n\ts_mov_b32 m0, %0"
+                   : "=&s"(saved)
                    : "s"(stage_w), "i"(4096 * k), "v"(src)
-                   : "memory", "m0");
+                   : "memory", "scc");
     }
   };
   auto stage_of = [&](int q) __attribute__((always_inline)) -> uint32_t {  // pair q's stage + 1 KiB w
@@ -500,18 +502,22 @@ __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams 
       const uint32_t off = (dmap[k / 2] >> (16 * (k % 2))) & 511u;
       if (ty == 3) {
         const uint8_t* src = p.k_scales + ((uint64_t)(uint32_t)sl * (uint32_t)p.k_scale_stride + off);
-        asm volatile("s_add_u32 m0, %0, %1\n\tglobal_load_lds_ubyte %2, off"
-                     :
+        uint32_t saved;
+        asm volatile("s_mov_b32 %0, m0\n\ts_add_u32 m0, %1, %2\n\ts_mov_b32 %0, %0\n\t"
+                     "global_load_lds_ubyte %3, off\n\ts_mov_b32 m0, %0"
+                     : "=&s"(saved)
                      : "s"(base), "i"(1024 * m), "v"(src)
-                     : "memory", "m0");
+                     : "memory", "scc");
       } else {
         const uint8_t* src = ty == 2 ? p.k_cache + ((uint64_t)(uint32_t)sl * (uint32_t)p.k_row_stride + off)
                                      : p.v_cache + ((uint64_t)(uint32_t)sl * (uint32_t)p.v_row_stride +
                                                     (uint32_t)(256 * ty) + off);
-        asm volatile("s_add_u32 m0, %0, %1\n\tglobal_load_lds_dwordx4 %2, off"
-                     :
+        uint32_t saved;
+        asm volatile("s_mov_b32 %0, m0\n\ts_add_u32 m0, %1, %2\n\ts_mov_b32 %0, %0\n\t"
+                     "global_load_lds_dwordx4 %3, off\n\ts_mov_b32 m0, %0"
+                     : "=&s"(saved)
                      : "s"(base), "i"(4096 * m), "v"(src)
-                     : "memory", "m0");
+                     : "memory", "scc");
       }
     }
   };

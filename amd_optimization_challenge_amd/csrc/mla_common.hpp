@@ -206,38 +206,31 @@ __device__ __forceinline__ uint2 quant8_fp8(uint4 v, Fp8Quant q) {
 // It is issued through inline asm so the compiler does not add conservative
 // vmcnt(0) waits before LDS reads and barriers: completion is tracked with
 // explicit wait_vmcnt<N>() calls, N = vector-memory ops issued after the one
-// that must have landed (vmcnt retires in order).  M0 is declared clobbered
-// (the compiler sets it again wherever it needs its own value).
+// that must have landed (vmcnt retires in order).
+// M0 is a reserved register the compiler assumes unchanged across inline asm,
+// so each DMA saves it and puts it back; an SALU write of M0 needs one wait
+// state before an LDS-DMA reads it, given here by an SALU no-op (SALU issue
+// costs the wave next to nothing, an s_nop a full issue slot).
 // The LDS offset is wave-uniform at every call site; readfirstlane states that
 // for the compiler, whose divergence analysis can otherwise leave it in a VGPR,
 // which the "s" constraint cannot take.
+#define MLA_LDS_DMA(INSN)                                                                          \
+  uint32_t saved;                                                                                  \
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_mov_b32 %0, %0\n\t" INSN " %2, off\n\t" \
+               "s_mov_b32 m0, %0"                                                                  \
+               : "=&s"(saved)                                                                      \
+               : "s"(__builtin_amdgcn_readfirstlane(lds_off)), "v"(g)                             \
+               : "memory")
 __device__ __forceinline__ void dma16_to_lds(const void* g, uint32_t lds_off) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
-               :
-               : "s"(__builtin_amdgcn_readfirstlane(lds_off)), "v"(g)
-               : "memory", "m0");
+  MLA_LDS_DMA("global_load_lds_dwordx4");
 }
-__device__ __forceinline__ void dma4_to_lds(const void* g, uint32_t lds_off) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off"
-               :
-               : "s"(__builtin_amdgcn_readfirstlane(lds_off)), "v"(g)
-               : "memory", "m0");
-}
+__device__ __forceinline__ void dma4_to_lds(const void* g, uint32_t lds_off) { MLA_LDS_DMA("global_load_lds_dword"); }
 // two bytes per lane (2-byte aligned source): lane l's bytes land,
 // zero-extended, in the dword at M0 + 4 l
-__device__ __forceinline__ void dma2_to_lds(const void* g, uint32_t lds_off) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_ushort %1, off"
-               :
-               : "s"(__builtin_amdgcn_readfirstlane(lds_off)), "v"(g)
-               : "memory", "m0");
-}
+__device__ __forceinline__ void dma2_to_lds(const void* g, uint32_t lds_off) { MLA_LDS_DMA("global_load_lds_ushort"); }
 // one byte per lane: lane l's byte lands, zero-extended, in the dword at M0 + 4 l
-__device__ __forceinline__ void dma1_to_lds(const void* g, uint32_t lds_off) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_ubyte %1, off"
-               :
-               : "s"(__builtin_amdgcn_readfirstlane(lds_off)), "v"(g)
-               : "memory", "m0");
-}
+__device__ __forceinline__ void dma1_to_lds(const void* g, uint32_t lds_off) { MLA_LDS_DMA("global_load_lds_ubyte"); }
+#undef MLA_LDS_DMA
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");

@@ -366,7 +366,9 @@ def blocks_per_cu(num_heads: int, kv_mode: int) -> int:
 def target_items(batch: int, num_heads: int, kv_mode: int, num_cu: int) -> int:
     """Work items the planner aims for (csrc/abi.hip target_items_for)."""
     slots = num_cu * blocks_per_cu(num_heads, kv_mode)
-    return min(max(slots, 2 * batch), 4 * slots)
+    if batch < slots:
+        return slots
+    return min(max(batch, slots * 3 // 2), 4 * slots)
 
 
 def workspace_layout(batch: int, num_heads: int, kv_mode, num_cu: int) -> dict:

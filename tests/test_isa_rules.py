@@ -1,5 +1,6 @@
-"""Wait-state hazards of the hand-written MFMAs of the H = 128 kernels.
+"""Rules the built gfx950 code objects must keep (llvm-objdump of our own build).
 
+1. Wait-state hazards of the hand-written MFMAs of the H = 128 kernels.
 decode_h128.hip issues its MFMAs by inline asm (each must keep its slot of the
 static schedule), so the compiler's hazard recognizer does not see them and
 the kernel must provide their wait states itself.  This test reads the
@@ -14,6 +15,11 @@ build) and checks, along every control-flow path (branch targets included):
   chain on those registers.
 
 s_nop N counts N + 1 wait states, every other instruction one.
+
+2. Every LDS-DMA (global_load_lds_*) follows the last write of M0 by at least
+one wait state (gfx9-family rule for an SALU write of M0 read by an LDS DMA).
+3. No scalar-memory stores, atomics or cache write-backs in any kernel.
+4. No packed-FP32 add/mul/fma (the build disables their formation).
 """
 import os
 import re
@@ -22,7 +28,8 @@ import subprocess
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-OBJ = os.path.join(ROOT, "amd_optimization_challenge_amd", "_build", "decode_h128.o")
+BUILD = os.path.join(ROOT, "amd_optimization_challenge_amd", "_build")
+OBJ = os.path.join(BUILD, "decode_h128.o")
 LLVM = "/opt/rocm/llvm/bin"
 PRE_WS, POST_WS = 2, 20
 
@@ -183,3 +190,57 @@ def test_checker_flags_planted_hazards():
     p = prog(loop)
     p[-1] = (p[-1][0], "s_cbranch_scc1", "", 4)
     assert check_function(p)
+
+
+def _objects(tmp_path):
+    if not os.path.isdir(BUILD) or not any(f.endswith(".o") for f in os.listdir(BUILD)):
+        pytest.skip("library not built (run __graft_entry__.build())")
+    if not all(os.path.exists(f"{LLVM}/{t}") for t in ("llvm-objcopy", "clang-offload-bundler", "llvm-objdump")):
+        pytest.skip("ROCm LLVM tools not found")
+    out = {}
+    for f in sorted(os.listdir(BUILD)):
+        if f.endswith(".o"):
+            d = tmp_path / f[:-2]
+            d.mkdir()
+            try:
+                out[f] = parse(disassemble(os.path.join(BUILD, f), str(d)))
+            except subprocess.CalledProcessError as e:
+                if b".hip_fatbin' not found" in (e.stderr or b""):
+                    continue  # host code only
+                raise
+    assert "decode_h128.o" in out and "decode.o" in out, sorted(out)
+    return out
+
+
+def m0_wait_violations(insns):
+    """LDS-DMAs issued with no instruction between them and the last M0 write."""
+    bad = []
+    for i, (_, mnem, args, _) in enumerate(insns):
+        if mnem.startswith("global_load_lds") and i > 0:
+            pm, pa = insns[i - 1][1], insns[i - 1][2]
+            if pm.startswith("s_") and pa.split(",")[0].strip() == "m0":
+                bad.append(f"{pm} {pa} directly before {mnem} {args}")
+    return bad
+
+
+FORBIDDEN_SCALAR = ("s_store", "s_buffer_store", "s_scratch_store", "s_atomic", "s_buffer_atomic", "s_dcache_wb")
+FORBIDDEN_PACKED = ("v_pk_add_f32", "v_pk_mul_f32", "v_pk_fma_f32")
+
+
+def test_code_object_rules(tmp_path):
+    report = []
+    for obj, funcs in _objects(tmp_path).items():
+        for name, insns in funcs.items():
+            report += [f"{obj} {name}: {b}" for b in m0_wait_violations(insns)]
+            for _, mnem, args, _ in insns:
+                if mnem.startswith(FORBIDDEN_SCALAR) or mnem in FORBIDDEN_PACKED:
+                    report.append(f"{obj} {name}: {mnem} {args}")
+    assert not report, "\n".join(report[:20])
+
+
+def test_m0_rule_checker():
+    ok = [(0, "s_mov_b32", "s4, m0", None), (4, "s_mov_b32", "m0, s6", None), (8, "s_mov_b32", "s4, s4", None),
+          (12, "global_load_lds_dwordx4", "v[2:3], off", None)]
+    bad = [ok[0], ok[1], (8, "global_load_lds_dwordx4", "v[2:3], off", None)]
+    assert not m0_wait_violations(ok)
+    assert m0_wait_violations(bad)
