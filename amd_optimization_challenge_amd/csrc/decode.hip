@@ -126,7 +126,7 @@ struct H16 {
   static constexpr int BLOCKS_PER_CU = (VF == 1 || KF == 2) ? 1 : 2;
   // DMA issue: waves RW0..3 gather rows.  fp4 K + fp8 V: wave 0 gathers the
   // 18 scale bytes of every token (SCW = 1); fp4 K = V: every wave gathers rows
-  // and scale byte columns j = w + 4k (SCW = 4), so no wave issues a long burst
+  // and scale dword columns j = w + 4k (SCW = 4), so no wave issues a long burst
   static constexpr int RW0 = (KF == 1 && VF == 1) ? 1 : 0;
   static constexpr int SCW = KF == 0 ? 0 : (VF == 1 ? 1 : 4);
   static constexpr int NRW = 4 - RW0;
@@ -137,7 +137,7 @@ struct H16 {
   static constexpr int PST = 68;                               // f32 P row stride (P32): 64 tokens + 4
   static constexpr int NSL = 2 * S;                            // slot stages (slots lead rows by S tiles)
   static constexpr int OFF_SLOT = S * STAGE;                   // [NSL][64] int32 cache slots
-  static constexpr int SCST = kMxBlocks * 256;                 // e8m0 stage: [18 blocks][64 tokens] dwords
+  static constexpr int SCST = kScWin * 256;                    // e8m0 stage: [5][64 tokens] dwords
   static constexpr int OFF_SC = OFF_SLOT + NSL * 256;          // [S] e8m0 stages (KF == 1)
   static constexpr int OFF_P = OFF_SC + (KF == 1 ? S * SCST : 0);
   static constexpr int P_BYTES = P32 ? 16 * PST * 4 : 2 * 4 * 16 * 16;  // f32 [h][token] | fp8 [term][g][h][16]
@@ -222,19 +222,21 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
       else if (u < C::NW) dma16_to_lds(p.v_cache + (int64_t)sl[k] * p.v_row_stride + co[k], sbase + 1024 * u);
     }
   };
-  // fp4 K scales: the e8m0 bytes of token `lane` of tile t, one byte per lane
-  // and instruction; byte j lands in dword j * 64 + lane of the tile's scale
-  // stage (sub-dword LDS-DMA writes one dword per lane).  Byte columns j = w +
-  // SCW k are this wave's.
+  // fp4 K scales: the 18 e8m0 bytes of token `lane` of tile t as 5 dwords
+  // (kScWin), dword j = blocks 4j .. 4j + 3 (j < 4) and blocks 14 .. 17 (j =
+  // 4, from byte 14: every read stays inside the row); dword j lands at
+  // j * 64 + lane of the tile's scale stage.  A row starts at any byte (the
+  // scale stride is free), so these are unaligned dword reads, which gfx950
+  // serves for global memory.  Columns j = w + SCW k are this wave's.
   auto issue_scales = [&](int t) __attribute__((always_inline)) {
     if constexpr (KF == 1) {
       if (w < C::SCW) {
         const uint8_t* srow = p.k_scales + (int64_t)slot_of(t, lane) * p.k_scale_stride;
         const uint32_t sb = lds0 + C::OFF_SC + (t % C::S) * C::SCST;
 #pragma unroll
-        for (int k = 0; k < (kMxBlocks + C::SCW - 1) / C::SCW; ++k) {
+        for (int k = 0; k < (kScWin + C::SCW - 1) / C::SCW; ++k) {
           const int j = w + C::SCW * k;
-          if (j < kMxBlocks) dma1_to_lds(srow + j, sb + 256 * j);
+          if (j < kScWin) dma4_to_lds(srow + (j < 4 ? 4 * j : 14), sb + 256 * j);
         }
       }
     }
@@ -243,16 +245,15 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
   auto wait_tile = [&](int k) __attribute__((always_inline)) {
     constexpr int SL = IDX ? 1 : 0;  // wave 0 issues one slot DMA per group
     if constexpr (KF == 1 && C::SCW == 4) {
-      // rows: NA for waves < NAW, else NA - 1; scale columns: 5 for waves 0, 1, else 4
-      constexpr int SC0 = (kMxBlocks + 3) / 4, SC1 = kMxBlocks / 4, R = kMxBlocks % 4;
-      static_assert(C::RW0 == 0 && C::NAW == 3 && R == 2, "per-wave DMA counts");
-      if (w == 0) wait_groups<C::NA + SC0 + SL>(k);
-      else if (w == 1) wait_groups<C::NA + SC0>(k);
-      else if (w == 2) wait_groups<C::NA + SC1>(k);
-      else wait_groups<C::NA - 1 + SC1>(k);
+      // rows: NA for waves < NAW, else NA - 1; scale columns: 2 for wave 0, else 1
+      static_assert(C::RW0 == 0 && C::NAW == 3 && kScWin == 5, "per-wave DMA counts");
+      if (w == 0) wait_groups<C::NA + 2 + SL>(k);
+      else if (w == 1) wait_groups<C::NA + 1>(k);
+      else if (w == 2) wait_groups<C::NA + 1>(k);
+      else wait_groups<C::NA - 1 + 1>(k);
     } else if constexpr (KF == 1) {
-      // wave 0: one slot DMA + 18 scale DMAs per group
-      if (w == 0) wait_groups<kMxBlocks + SL>(k);
+      // wave 0: one slot DMA + the 5 scale DMAs per group
+      if (w == 0) wait_groups<kScWin + SL>(k);
       else if (w - C::RW0 < C::NAW) wait_groups<C::NA>(k);
       else wait_groups<C::NA - 1>(k);
     } else {
@@ -469,7 +470,9 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
         issue_scales(ti + C::S - 1);
       }
       const uint8_t* kt = smem + st * C::STAGE;
-      const uint8_t* sct = smem + C::OFF_SC + st * C::SCST;  // e8m0 of (token t, block j) at 256 j + 4 t
+      // e8m0 of (token t, block j): byte j & 3 of dword (j >> 2, t) at 256 (j >> 2)
+      // + 4 t (j < 16), byte j - 14 of dword (4, t) (j = 16, 17)
+      const uint8_t* sct = smem + C::OFF_SC + st * C::SCST;
 
       // ---- scores: rows i = l16 of this wave's slice, 16x16x128 MFMAs ----------
       v4f s = v4f{0.f, 0.f, 0.f, 0.f};
@@ -502,7 +505,7 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
           for (int ks = 0; ks < 5; ++ks) {
             const int blk = 4 * ks + g;
             ka[ks] = blk < kMxBlocks ? ld_v4_as_v8(kp + 16 * blk) : v8i{0, 0, 0, 0, 0, 0, 0, 0};
-            ksc[ks] = blk < kMxBlocks ? (int)sp[256 * blk] : 127;
+            ksc[ks] = blk < kMxBlocks ? (int)sp[256 * ks + (ks < 4 ? g : 2 + g)] : 127;  // blk = 4 ks + g
           }
 #pragma unroll
           for (int ks = 0; ks < 5; ++ks) s = mfma16_f4f8(ka[ks], ksc[ks], qv[ks], s);
@@ -656,16 +659,21 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
         }
         const int trow = l16 < 8 ? 8 * g + l16 : 24 + 8 * g + l16;
         const uint32_t va = lds0 + st * C::STAGE + trow * C::KST + 64 * w;
-        const int* sce = reinterpret_cast<const int*>(sct);
+        // dword (w, t): the e8m0 of this wave's blocks 4w .. 4w + 3 (dims 128w ..)
+        const int* se = reinterpret_cast<const int*>(sct) + 64 * w;
+        const int4 e0 = *reinterpret_cast<const int4*>(se + 8 * g);
+        const int4 e1 = *reinterpret_cast<const int4*>(se + 8 * g + 4);
+        const int4 e2 = *reinterpret_cast<const int4*>(se + 32 + 8 * g);
+        const int4 e3 = *reinterpret_cast<const int4*>(se + 36 + 8 * g);
+        const uint32_t ed[16] = {(uint32_t)e0.x, (uint32_t)e0.y, (uint32_t)e0.z, (uint32_t)e0.w,
+                                 (uint32_t)e1.x, (uint32_t)e1.y, (uint32_t)e1.z, (uint32_t)e1.w,
+                                 (uint32_t)e2.x, (uint32_t)e2.y, (uint32_t)e2.z, (uint32_t)e2.w,
+                                 (uint32_t)e3.x, (uint32_t)e3.y, (uint32_t)e3.z, (uint32_t)e3.w};
 #pragma unroll
-        for (int jl = 0; jl < 4; ++jl) {
-          const int* se = sce + 64 * (4 * w + jl);  // e8m0 of block 4w + jl (dims 32(4w + jl) ..)
-          const int4 e0 = *reinterpret_cast<const int4*>(se + 8 * g);
-          const int4 e1 = *reinterpret_cast<const int4*>(se + 8 * g + 4);
-          const int4 e2 = *reinterpret_cast<const int4*>(se + 32 + 8 * g);
-          const int4 e3 = *reinterpret_cast<const int4*>(se + 36 + 8 * g);
-          const int ev[16] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w,
-                              e2.x, e2.y, e2.z, e2.w, e3.x, e3.y, e3.z, e3.w};
+        for (int jl = 0; jl < 4; ++jl) {  // block 4w + jl (dims 32(4w + jl) ..): byte jl
+          int ev[16];
+#pragma unroll
+          for (int k = 0; k < 16; ++k) ev[k] = (int)((ed[k] >> (8 * jl)) & 0xFFu);
           uint32_t bw[8];
 #pragma unroll
           for (int k = 0; k < 16; k += 2)

@@ -12,6 +12,7 @@ constexpr int kQKDim = 576;       // 512 latent + 64 rope
 constexpr int kVDim = 512;        // latent part, used as V
 constexpr int kFp4RowBytes = 288; // 576 e2m1 values, two per byte
 constexpr int kMxBlocks = 18;     // 576 / 32 e8m0 scales per row
+constexpr int kScWin = 5;         // dwords that hold a row's 18 e8m0 bytes (LDS-DMA)
 constexpr int kTile = 64;         // tokens staged per LDS tile
 
 // ---- plan layout (int32 words inside the workspace) -------------------------
