@@ -315,6 +315,21 @@ struct MixSched {
   static_assert(H128Sched::kStageFree == 20 && H128Sched::kBarrier == 45, "barrier slots");
 };
 
+// What each iteration of a pair runs: QK, softmax and PV are 1 (always), 0
+// (never) or 2 (where the tile or pair exists: a runtime test per MFMA and
+// softmax step, which costs the schedule about a thousand cycles per
+// iteration); softmax 3 = never, but its half of the P' operand is zeroed
+// (the pair's PV reads it).  K1: the second iteration runs (1), is skipped
+// (0) or runs while q <= npair (2).
+template <int Q0, int S0, int P0, int Q1, int S1, int P1, int K1>
+struct PairKind {
+  static constexpr int qk(int it) { return it ? Q1 : Q0; }
+  static constexpr int sm(int it) { return it ? S1 : S0; }
+  static constexpr int pv(int it) { return it ? P1 : P0; }
+  static constexpr int k1 = K1;
+  static constexpr bool edge = !(Q0 == 1 && S0 == 1 && P0 == 1 && Q1 == 1 && S1 == 1 && P1 == 1 && K1 == 1);
+};
+
 // MIX: the two-cache mode (fp4 K + e8m0, fp8 V); else the fp8 cache
 template <bool IDX, bool MIX>
 __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams p) {
@@ -735,14 +750,15 @@ __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams 
   v16f sa, sb;  // QK accumulators of tiles of parity 0 / 1
   int rs[2] = {0, 0};  // slots of the next row DMAs (read two slots ahead)
   int mrs = 0;         // two-cache mode: the same (one at a time)
-  // GUARD: a pair at an edge of the pipeline, whose QK, softmax and PV parts
-  // run only where their tile (pair) exists: t < n; 1 <= t <= n; pair j >= 0,
-  // 2j < n.  Fragment loads and slot-index DMAs run everywhere (their
-  // addresses stay inside the ring and the item).  DM: the rows of pair q + 2
-  // (which exist iff q + 2 < npair) are fetched always (1), never (0), or as
-  // that test says (2).
-  auto pair = [&](auto guard_tag, auto dm_tag, int q) __attribute__((always_inline)) {
-    constexpr bool GUARD = decltype(guard_tag)::value;
+  // Kind (PairKind): which QK, softmax and PV parts run; at the edges of the
+  // pipeline a part runs only where its tile (pair) exists: t < n; 1 <= t <=
+  // n; pair j >= 0, 2j < n.  Fragment loads and slot-index DMAs run everywhere
+  // (their addresses stay inside the ring and the item).  DM: the rows of pair
+  // q + 2 (which exist iff q + 2 < npair) are fetched always (1), never (0), or
+  // as that test says (2).
+  auto pair = [&](auto kind_tag, auto dm_tag, int q) __attribute__((always_inline)) {
+    using PK = decltype(kind_tag);
+    constexpr bool GUARD = PK::edge;
     constexpr int DM = decltype(dm_tag)::value;
     asm volatile("" : "+s"(q));  // nothing that depends on q is precomputed (and kept live) outside the pair
     const bool dmas = DM == 1 || (DM == 2 && q + 2 < npair);
@@ -776,10 +792,11 @@ __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams 
         r_lo = w_lo;
         rsc = wsc;
       }
+      constexpr int KQ = PK::qk(IT), KS = PK::sm(IT), KP = PK::pv(IT);
       // 1. the slot's MFMA
-      if constexpr (SC::is_qk(i)) {
+      if constexpr (SC::is_qk(i) && KQ != 0) {
         constexpr int g = i / 3;
-        if (!GUARD || t < n) {
+        if (KQ == 1 || t < n) {
           if constexpr (MIX) {
             const int sa = g < 4 ? sc_lo[g & 3] : g < 8 ? sc_hi[g & 3] : sc8;
             if constexpr (g == 0) qk4_first(s_qk, kf4[0], qv[0], sa);
@@ -789,9 +806,9 @@ __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams 
             else qk_acc(s_qk, kf[g % 3], qv[g]);
           }
         }
-      } else {
+      } else if constexpr (!SC::is_qk(i) && KP != 0) {
         constexpr int g = i / 3, term = i % 3 - 1;
-        if (!GUARD || (j >= 0 && 2 * j < n)) pv_mfma(o[8 * H + g], vf[g % 2], term == 0 ? r_hi : r_lo, rsc);
+        if (KP == 1 || (j >= 0 && 2 * j < n)) pv_mfma(o[8 * H + g], vf[g % 2], term == 0 ? r_hi : r_lo, rsc);
       }
       // 2. barriers: pair q - 2's stage free (every wave's last V^T read of it
       // done); pair q + 1 published (its rows landed)
@@ -889,25 +906,33 @@ __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams 
       }
       // 5. one softmax step of tile t - 1 (a tile past the item leaves its half
       // of the operand zero)
-      if constexpr (i >= 2 && i < 2 + SC::kSoftSteps) {
-        if (!GUARD || (t >= 1 && t <= n)) {
-          softmax_step(Ic<i - 2>{}, Ic<1 - IT>{}, t - 1, s_sm, w_hi, w_lo);
-        } else if constexpr (i == 2) {
+      if constexpr (i >= 2 && i < 2 + SC::kSoftSteps && KS != 0) {
+        auto zero_half = [&]() __attribute__((always_inline)) {
 #pragma unroll
           for (int qd = 0; qd < 4; ++qd) {
             w_hi[4 * (1 - IT) + qd] = 0;
             w_lo[4 * (1 - IT) + qd] = 0;
           }
+        };
+        // an iteration with no PV has no MFMA in slot 1: 8 more wait states
+        // before the first read of the QK result
+        if constexpr (i == 2 && KP == 0) asm volatile("s_nop 7" : "+v"(s_sm));
+        if constexpr (KS == 1) {
+          softmax_step(Ic<i - 2>{}, Ic<1 - IT>{}, t - 1, s_sm, w_hi, w_lo);
+        } else if constexpr (KS == 2) {
+          if (t >= 1 && t <= n) softmax_step(Ic<i - 2>{}, Ic<1 - IT>{}, t - 1, s_sm, w_hi, w_lo);
+          else if constexpr (i == 2) zero_half();
+        } else if constexpr (i == 2) {
+          zero_half();
         }
       }
       __builtin_amdgcn_sched_barrier(0);
     };
     static_for<0, SC::kSlots>(slot);
     // the last pair's second iteration has no work (no QK, softmax or PV tile)
-    if (!GUARD || q <= npair) static_for<SC::kSlots, 2 * SC::kSlots>(slot);
+    if (PK::k1 == 1 || (PK::k1 == 2 && q <= npair)) static_for<SC::kSlots, 2 * SC::kSlots>(slot);
   };
-  const std::true_type Y{};
-  const std::false_type N{};
+  const PairKind<1, 1, 1, 1, 1, 1, 1> N{};  // full pairs
   const Ic<0> Z{};
   const Ic<1> A{};
   const Ic<2> R{};
@@ -962,11 +987,15 @@ __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams 
       // then those that drain the pipeline (the last PV pair, npair - 1, runs in
       // pairs npair and npair + 1)
       int q = 0;
-      pair(Y, R, 0);
-      pair(Y, R, 1);
+      // Edge pairs, valid for every n >= 1: QK runs unconditionally (a tile past
+      // the item only fills an accumulator whose softmax never runs), PV runs
+      // wherever its pair exists (j >= 0 is fixed per pair; in the tail every
+      // PV pair has 0 <= 2j < n), and only the softmax keeps a runtime test.
+      pair(PairKind<1, 0, 0, 1, 1, 0, 1>{}, R, 0);
+      pair(PairKind<1, 2, 0, 1, 2, 1, 1>{}, R, 1);
       for (q = 2; q + 2 < npair; ++q) pair(N, A, q);  // q + 2 < npair implies 2q + 1 < n
       for (; 2 * q + 1 < n; ++q) pair(N, Z, q);
-      for (; q <= npair + 1; ++q) pair(Y, R, q);
+      for (; q <= npair + 1; ++q) pair(PairKind<1, 2, 1, 1, 2, 1, 2>{}, R, q);
     }
     // a flagged head on any wave: run the item again from the running maxima
     wait_vmcnt<0>();
