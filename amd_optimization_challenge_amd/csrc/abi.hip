@@ -98,6 +98,29 @@ int target_items_for(int batch, int num_heads, int kv_mode, int num_cu) {
   return t < 4 * slots ? t : 4 * slots;
 }
 
+// Contiguous rows (no kv_indices) at 16 heads stream well from one work-group
+// per CU, so while the batch is below the CU count the target is one item per
+// CU rather than per slot (fewer, longer pieces: fewer prologues and
+// partials), and from there up the chunk (longest piece) is at least 1024
+// tokens: a two-way split of 1024-token sequences costs more in prologues and
+// partial outputs than the idle slots it fills.  No sequence is cut into more
+// than 32 pieces: the combine folds a sequence's pieces 8 loads at a time per
+// thread, on 4 work-groups per 16 heads, so 64 pieces cost more in that serial
+// tail than the shorter items save.  On the task's shapes (mxfp4 cache, whole
+// call) this took 256 x 1024 from 71 to 61 us, 32 x 8192 from 67 to 64 and
+// 4 x 8192 from 38.5 to 35.9; indexed caches keep target_items_for, their
+// scattered rows need both slots of a CU in flight (128 x 4096: 97 us at one
+// item per slot, 122 at one per CU).
+PlanTarget plan_target_for(int batch, int num_heads, int kv_mode, int num_cu, bool contiguous) {
+  PlanTarget t{target_items_for(batch, num_heads, kv_mode, num_cu), kPlanMinChunk, 0};
+  if (contiguous && num_heads == 16) {
+    if (batch < num_cu) t.items = num_cu < t.items ? num_cu : t.items;
+    else t.min_chunk = 1024;
+    t.max_splits = 32;
+  }
+  return t;
+}
+
 WsLayout workspace_layout(int batch, int num_heads, int kv_mode, int num_cu) {
   WsLayout L;
   // the planner emits at most target + batch items; the layout is sized for the
@@ -225,7 +248,7 @@ int mla_quant_fp8_per_tensor(const void* x_bf16, int64_t n, void* out_fp8, float
   uint32_t* partials = static_cast<uint32_t*>(workspace);
   int nb = 0;
   hipError_t e = launch_amax(static_cast<const uint16_t*>(x_bf16), n, partials, &nb, nullptr, nullptr, 0, 1,
-                             0, 0, nullptr, s);
+                             PlanTarget{0, kPlanMinChunk, 0}, 0, nullptr, s);
   if (e != hipSuccess) return hip_fail(e, "amax launch");
   e = launch_quant_fp8(static_cast<const uint16_t*>(x_bf16), n, partials, nb,
                        static_cast<uint8_t*>(out_fp8), out_scale, s);
@@ -318,7 +341,7 @@ int mla_plan(const int32_t* kv_indptr, int batch, int q_seq_len, int num_heads, 
     return set_error(MLA_ERR_WORKSPACE_TOO_SMALL, "workspace needs %lld bytes (got %lld)", (long long)L.total,
                 (long long)workspace_bytes);
   int32_t* plan = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + L.plan_off);
-  hipError_t e = launch_plan(kv_indptr, batch, q_seq_len, target_items_for(batch, num_heads, kv_mode, ncu),
+  hipError_t e = launch_plan(kv_indptr, batch, q_seq_len, plan_target_for(batch, num_heads, kv_mode, ncu, false),
                              L.max_items, plan,
                              static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(e, "plan launch");
@@ -399,7 +422,8 @@ int mla_decode_fwd(const void* q_bf16, const void* k_cache, int64_t k_row_stride
   uint32_t* partials = reinterpret_cast<uint32_t*>(ws + L.quant_off);
   int nb = 0;
   if (kv_mode == MLA_KV_BF16) {  // a16w16: Q is used as it is, no amax pass
-    hipError_t e = launch_plan(kv_indptr, batch, q_seq_len, target_items_for(batch, num_heads, kv_mode, ncu),
+    hipError_t e = launch_plan(kv_indptr, batch, q_seq_len,
+                               plan_target_for(batch, num_heads, kv_mode, ncu, kv_indices == nullptr),
                                L.max_items, reinterpret_cast<int32_t*>(ws + L.plan_off), s);
     if (e != hipSuccess) return hip_fail(e, "plan launch");
     p.q_bf16 = static_cast<const uint16_t*>(q_bf16);
@@ -411,7 +435,7 @@ int mla_decode_fwd(const void* q_bf16, const void* k_cache, int64_t k_row_stride
   }
   hipError_t e = launch_amax(static_cast<const uint16_t*>(q_bf16), n, partials, &nb, kv_indptr,
                              static_cast<const int32_t*>(kv_indices), batch, q_seq_len,
-                             target_items_for(batch, num_heads, kv_mode, ncu),
+                             plan_target_for(batch, num_heads, kv_mode, ncu, kv_indices == nullptr),
                              L.max_items, reinterpret_cast<int32_t*>(ws + L.plan_off), s);
   if (e != hipSuccess) return hip_fail(e, "amax+plan launch");
   if (num_heads == 16) {
@@ -459,7 +483,8 @@ int mla_decode_fwd_a16w8(const void* q_bf16, const void* k_cache, int64_t k_row_
                      lse_out, &p, &L);
   if (rc) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  hipError_t e = launch_plan(kv_indptr, batch, q_seq_len, target_items_for(batch, num_heads, kv_mode, ncu),
+  hipError_t e = launch_plan(kv_indptr, batch, q_seq_len,
+                             plan_target_for(batch, num_heads, kv_mode, ncu, kv_indices == nullptr),
                              L.max_items, reinterpret_cast<int32_t*>(ws + L.plan_off), s);
   if (e != hipSuccess) return hip_fail(e, "plan launch");
   p.q_bf16 = static_cast<const uint16_t*>(q_bf16);  // no partials: each work-group scales its own Q rows

@@ -32,13 +32,27 @@ struct WsLayout {
   int target_items;
 };
 
+// What the split planner aims for: `items` work items, a chunk (longest
+// piece) of at least `min_chunk` tokens (a multiple of 64), and, when
+// max_splits > 0, no sequence cut into more than max_splits pieces.
+struct PlanTarget {
+  int items;
+  int min_chunk;
+  int max_splits;
+};
+// smallest chunk by default: a piece of two tiles at least, so that short
+// batches are not cut into one-tile items whose fixed costs (ring start,
+// partial write, combine input) exceed their work
+constexpr int kPlanMinChunk = 128;
+
 int target_items_for(int batch, int num_heads, int kv_mode, int num_cu);
+PlanTarget plan_target_for(int batch, int num_heads, int kv_mode, int num_cu, bool contiguous);
 WsLayout workspace_layout(int batch, int num_heads, int kv_mode, int num_cu);
 
 // quant.hip
 hipError_t launch_amax(const uint16_t* x, int64_t n, uint32_t* partials, int* nblocks,
                        const int32_t* kv_indptr, const int32_t* kv_indices, int batch, int qlen,
-                       int target_items, int max_items, int32_t* plan, hipStream_t stream);
+                       PlanTarget target, int max_items, int32_t* plan, hipStream_t stream);
 // partials: 16-byte aligned, nblocks <= kAmaxMaxBlocks maxima (read four at a
 // time, so up to three words past nblocks are read and ignored)
 hipError_t launch_quant_fp8(const uint16_t* x, int64_t n, const uint32_t* partials, int nblocks,
@@ -46,7 +60,7 @@ hipError_t launch_quant_fp8(const uint16_t* x, int64_t n, const uint32_t* partia
 hipError_t launch_pack_mxfp4(const uint16_t* x, int64_t rows, int cols, int64_t x_stride,
                              uint8_t* packed, int64_t packed_stride, uint8_t* scales,
                              int64_t scale_stride, hipStream_t stream);
-hipError_t launch_plan(const int32_t* kv_indptr, int batch, int qlen, int target_items, int max_items,
+hipError_t launch_plan(const int32_t* kv_indptr, int batch, int qlen, PlanTarget target, int max_items,
                        int32_t* plan, hipStream_t stream);
 hipError_t launch_expand_pages(const int32_t* page_indptr, const int32_t* page_ids, const int32_t* last_page_lens,
                                int batch, int page_size, int64_t max_pages, int32_t* kv_indptr_out,

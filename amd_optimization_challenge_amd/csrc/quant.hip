@@ -19,16 +19,17 @@ namespace mla {
 // unsigned ordering of (bits & 0x7fff) for non-NaN inputs)
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ void build_plan(const int32_t* __restrict__ kv_indptr, int batch, int qlen,
-                                           int target_items, int max_items, int32_t* __restrict__ plan);
+                                           int target_items, int min_chunk, int max_splits, int max_items,
+                                           int32_t* __restrict__ plan);
 
 __global__ __launch_bounds__(256) void amax_kernel(const uint16_t* __restrict__ x, int64_t n,
                                                    uint32_t* __restrict__ partials, int nblocks,
                                                    const int32_t* __restrict__ kv_indptr,
                                                    const int32_t* __restrict__ kv_indices,
-                                                   int batch, int qlen, int target_items, int max_items,
-                                                   int32_t* __restrict__ plan) {
+                                                   int batch, int qlen, int target_items, int min_chunk,
+                                                   int max_splits, int max_items, int32_t* __restrict__ plan) {
   if ((int)blockIdx.x >= nblocks) {  // trailing block: split planner
-    build_plan(kv_indptr, batch, qlen, target_items, max_items, plan);
+    build_plan(kv_indptr, batch, qlen, target_items, min_chunk, max_splits, max_items, plan);
     return;
   }
   if (kv_indices != nullptr) {
@@ -264,7 +265,9 @@ __global__ __launch_bounds__(256) void append_kv_kernel(
 // with qlen = 1 a row is a sequence.  Below, "sequence b" means row b.
 // Sequence b is cut into n_b = max(1, ceil(L_b / chunk)) near-equal pieces.
 // For batch <= 256, chunk = the smallest multiple of 64 with sum_b n_b <=
-// target_items (binary search from c0 = max(128, 64 ceil(T / (64 target))),
+// target_items (binary search from c0 = max(min_chunk, 64 ceil(T / (64 target)),
+// and, when max_splits > 0, 64 ceil(Lmax / (64 max_splits)) for the longest
+// sequence Lmax),
 // T = all tokens; the longest sequence if no chunk fits), and the sequences
 // are laid out longest piece first so late-starting work-groups get the short
 // items.  For larger batches chunk = c0 and the order is the sequence order.
@@ -274,10 +277,6 @@ __global__ __launch_bounds__(256) void append_kv_kernel(
 // partial slot = its item index.
 // ---------------------------------------------------------------------------
 constexpr int kPlanSortMax = 256;
-// smallest chunk: a piece of two tiles at least, so that short batches are not
-// cut into one-tile items whose fixed costs (ring start, partial write, combine
-// input) exceed their work
-constexpr int kPlanMinChunk = 128;
 
 // sum / max of one non-negative int per thread over the 256-thread block
 // (`red` holds 4 ints; every thread gets the result)
@@ -352,14 +351,16 @@ __device__ __forceinline__ void emit_pieces(int4* __restrict__ items, int b, int
 // item back), so the plan costs one round trip to kv_indptr and no barriers.
 // Same plan as the block version below.
 __device__ __forceinline__ void build_plan_wave(const int32_t* __restrict__ kv_indptr, int batch, int qlen,
-                                                int target_items, int max_items, int32_t* __restrict__ plan) {
+                                                int target_items, int min_chunk, int max_splits, int max_items,
+                                                int32_t* __restrict__ plan) {
   const int lane = threadIdx.x & 63;
   const bool act = lane < batch;
   const int s0 = act ? row_start(kv_indptr, lane, qlen) : 0;
   const int L = act ? row_len(kv_indptr, lane, qlen) : 0;
   const unsigned hi64 = (unsigned)wave_sum(L >> 6), lo64 = (unsigned)wave_sum(L & 63);
   const int lmax = wave_max(L);
-  int lo = max(kPlanMinChunk / 64, (int)tiles_per_item(hi64, lo64, target_items));
+  int lo = max(min_chunk / 64, (int)tiles_per_item(hi64, lo64, target_items));
+  if (max_splits > 0) lo = max(lo, ((lmax + 63) / 64 + max_splits - 1) / max_splits);
   int hi = max(lo, (lmax + 63) / 64);
   const int L64 = (L + 63) >> 6;  // ceil(L / (64 m)) = ceil(L64 / m)
   while (lo < hi) {
@@ -402,9 +403,11 @@ __device__ __forceinline__ void build_plan_wave(const int32_t* __restrict__ kv_i
 }
 
 __device__ __forceinline__ void build_plan(const int32_t* __restrict__ kv_indptr, int batch, int qlen,
-                                           int target_items, int max_items, int32_t* __restrict__ plan) {
+                                           int target_items, int min_chunk, int max_splits, int max_items,
+                                           int32_t* __restrict__ plan) {
   if (batch <= 64) {
-    if (threadIdx.x < 64) build_plan_wave(kv_indptr, batch, qlen, target_items, max_items, plan);
+    if (threadIdx.x < 64)
+      build_plan_wave(kv_indptr, batch, qlen, target_items, min_chunk, max_splits, max_items, plan);
     return;
   }
   __shared__ int s_red[4];
@@ -422,10 +425,11 @@ __device__ __forceinline__ void build_plan(const int32_t* __restrict__ kv_indptr
     own_s0 = row_start(kv_indptr, b, qlen);
   }
   const unsigned hi64 = (unsigned)block_sum(t_hi, s_red), lo64 = (unsigned)block_sum(t_lo, s_red);
-  int chunk = 64 * max(kPlanMinChunk / 64, (int)tiles_per_item(hi64, lo64, target_items));
+  const int lmax = block_max(t_max, s_red);
+  int chunk = 64 * max(min_chunk / 64, (int)tiles_per_item(hi64, lo64, target_items));
+  if (max_splits > 0) chunk = max(chunk, 64 * (((lmax + 63) / 64 + max_splits - 1) / max_splits));
   if (batch <= kPlanSortMax) {
     // one sequence per thread: binary search on chunk / 64 in [c0 / 64, ceil(lmax / 64)]
-    const int lmax = block_max(t_max, s_red);
     const int L64 = (t_max + 63) >> 6;  // batch <= 256: t_max is this thread's own L
     int lo = chunk / 64, hi = max(lo, (lmax + 63) / 64);
     while (lo < hi) {
@@ -501,9 +505,9 @@ __device__ __forceinline__ void build_plan(const int32_t* __restrict__ kv_indptr
 }
 
 __global__ __launch_bounds__(256) void plan_kernel(const int32_t* __restrict__ kv_indptr, int batch, int qlen,
-                                                   int target_items, int max_items,
+                                                   int target_items, int min_chunk, int max_splits, int max_items,
                                                    int32_t* __restrict__ plan) {
-  build_plan(kv_indptr, batch, qlen, target_items, max_items, plan);
+  build_plan(kv_indptr, batch, qlen, target_items, min_chunk, max_splits, max_items, plan);
 }
 
 // ---------------------------------------------------------------------------
@@ -577,12 +581,13 @@ static int amax_blocks_for(int64_t n) {
 
 hipError_t launch_amax(const uint16_t* x, int64_t n, uint32_t* partials, int* nblocks,
                        const int32_t* kv_indptr, const int32_t* kv_indices, int batch, int qlen,
-                       int target_items, int max_items, int32_t* plan, hipStream_t stream) {
+                       PlanTarget target, int max_items, int32_t* plan, hipStream_t stream) {
   const int nb = amax_blocks_for(n);
   *nblocks = nb;
   const int grid = nb + (plan != nullptr ? 1 : 0);
   hipLaunchKernelGGL(amax_kernel, dim3(grid), dim3(256), 0, stream, x, n, partials, nb, kv_indptr,
-                     plan != nullptr ? kv_indices : nullptr, batch, qlen, target_items, max_items, plan);
+                     plan != nullptr ? kv_indices : nullptr, batch, qlen, target.items, target.min_chunk,
+                     target.max_splits, max_items, plan);
   return hipGetLastError();
 }
 
@@ -636,10 +641,10 @@ hipError_t launch_expand_pages(const int32_t* page_indptr, const int32_t* page_i
   return hipGetLastError();
 }
 
-hipError_t launch_plan(const int32_t* kv_indptr, int batch, int qlen, int target_items, int max_items,
+hipError_t launch_plan(const int32_t* kv_indptr, int batch, int qlen, PlanTarget target, int max_items,
                        int32_t* plan, hipStream_t stream) {
-  hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(256), 0, stream, kv_indptr, batch, qlen, target_items,
-                     max_items, plan);
+  hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(256), 0, stream, kv_indptr, batch, qlen, target.items,
+                     target.min_chunk, target.max_splits, max_items, plan);
   return hipGetLastError();
 }
 

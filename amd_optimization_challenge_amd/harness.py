@@ -30,7 +30,7 @@ test equipment: ``custom_kernel`` never calls it.  The L2 flush is the
 reference's 62.5 GiB ``randn`` (utils.py:198-200) unless a size is given.
 
     python -m amd_optimization_challenge_amd.harness {test,benchmark,leaderboard}
-           [--specs FILE] [--seed N] [--flush-mib N] [--max-repeats N]
+           [--specs FILE] [--seed N] [--flush-mib N] [--max-repeats N] [--kv-mode MODE]
 """
 from __future__ import annotations
 
@@ -363,6 +363,9 @@ def main(argv=None) -> int:
     ap.add_argument("--flush-mib", type=int, default=None, help="rewrite this many MiB instead of the 62.5 GiB randn")
     ap.add_argument("--max-repeats", type=int, default=None)
     ap.add_argument("--json", action="store_true", help="also print one JSON summary line")
+    ap.add_argument("--kv-mode", default=None,
+                    help="set config['kv_mode'] on every input (e.g. 'auto', 'mxfp4'); default: the key is absent "
+                         "and custom_kernel takes its a8w8 default")
     args = ap.parse_args(argv)
     if args.specs:
         with open(args.specs) as f:
@@ -373,13 +376,20 @@ def main(argv=None) -> int:
                     c.args["seed"] = mix_seed(c.args["seed"], args.seed)
     else:
         cases = task_cases("test" if args.mode == "test" else "benchmark", args.seed)
-    rc, results = run(args.mode, cases, flush=L2Flush(args.flush_mib), max_repeats=args.max_repeats,
+    kernel = None
+    if args.kv_mode is not None:
+        from .submission import custom_kernel
+
+        def kernel(data, kv_mode=args.kv_mode):
+            q, kv_data, qo_indptr, kv_indptr, config = data
+            return custom_kernel((q, kv_data, qo_indptr, kv_indptr, {**config, "kv_mode": kv_mode}))
+    rc, results = run(args.mode, cases, kernel=kernel, flush=L2Flush(args.flush_mib), max_repeats=args.max_repeats,
                       log=lambda s: print(s, flush=True))
     if args.json:
         summary = {k: (dataclasses.asdict(v) if isinstance(v, Stats) else v) for k, v in results.items()}
         means = [v.mean for v in results.values() if isinstance(v, Stats)]
-        print(json.dumps({"mode": args.mode, "status": rc, "geomean_us": geomean(means) / 1e3 if means else None,
-                          "cases": summary}), flush=True)
+        print(json.dumps({"mode": args.mode, "kv_mode": args.kv_mode, "status": rc,
+                          "geomean_us": geomean(means) / 1e3 if means else None, "cases": summary}), flush=True)
     return rc
 
 

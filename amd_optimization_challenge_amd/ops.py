@@ -371,6 +371,26 @@ def target_items(batch: int, num_heads: int, kv_mode: int, num_cu: int) -> int:
     return min(max(batch, slots * 3 // 2), 4 * slots)
 
 
+PLAN_MIN_CHUNK = 128
+
+
+def plan_target(batch: int, num_heads: int, kv_mode: int, num_cu: int, contiguous: bool = False) -> tuple:
+    """(items, min_chunk, max_splits) the planner aims for (csrc/abi.hip
+    plan_target_for): ``mla_plan`` and the indexed caches use ``target_items``,
+    a 128-token chunk floor and no split cap; the fused entry points on a
+    contiguous 16-head cache (no kv_indices) aim for one item per CU below
+    that many sequences, a 1024-token chunk floor from there up, and at most
+    32 pieces per sequence."""
+    items, min_chunk, max_splits = target_items(batch, num_heads, kv_mode, num_cu), PLAN_MIN_CHUNK, 0
+    if contiguous and num_heads == 16:
+        if batch < num_cu:
+            items = min(items, num_cu)
+        else:
+            min_chunk = 1024
+        max_splits = 32
+    return items, min_chunk, max_splits
+
+
 def workspace_layout(batch: int, num_heads: int, kv_mode, num_cu: int) -> dict:
     """Byte offsets of the workspace regions; ``total`` equals mla_workspace_bytes.
     Sized for the largest target over the kv modes (``target_items``);

@@ -17,6 +17,11 @@ caches shaped [pages, page_size, 1, row], ``kv_indptr`` over pages,
 ``config["kv_indices"]`` the page ids and ``config["kv_last_page_lens"]``.
 ``config["q_dtype"] = "bf16"`` takes the reference's a16w8 route (bf16 Q, fp8
 cache, 16 heads; TASK/reference.py:55-58 Q_DTYPE) instead of a8w8.
+``config["kv_mode"] = "auto"`` picks the cache by speed, as the reference's
+custom_kernel routes each (batch, kv_len) to its fastest path
+(mixed-mla/submission.py:626-644, MXFP4 Triton for the small shapes): see
+``auto_kv_mode``.  Without the key the route is a8w8 over the fp8 cache, the
+one the north-star tolerance (2e-2) holds for on every shape.
 There is no fallback: a missing library or an unsupported shape raises.
 """
 from __future__ import annotations
@@ -31,6 +36,22 @@ from .task import input_t, output_t
 DEFAULT_SM_SCALE = 1.0 / math.sqrt(576.0)
 
 
+def auto_kv_mode(num_heads: int, kv_data: dict) -> str:
+    """The fastest route whose cache is present.  At 16 heads the MXFP4 cache
+    (e2m1 K and V, 306 bytes a token against 576) wins on every task shape under
+    the leaderboard protocol (MI355X, whole call: 4 x 8192 38.9 us against 40.4
+    for fp8, 64 x 8192 90.1 against 130.9, 256 x 1024 62.1 against 84.3; 4 x
+    1024 ties at 25.9 / 25.5) and passes the task's check (rtol = atol = 0.1,
+    competitor_submissions/mi355x_reference/reference.py:372); bf16 Q (a16w8)
+    was slower than a8w8 on all eight.  At 128 heads the fp8 cache is the one
+    that reads fewest bytes (the mixed route reads both caches)."""
+    if num_heads == 16 and "mxfp4" in kv_data:
+        return "mxfp4"
+    if "fp8" in kv_data:
+        return "fp8"
+    raise ValueError("kv_mode 'auto' needs the fp8 or (at 16 heads) the mxfp4 cache in kv_data")
+
+
 def custom_kernel(data: input_t) -> output_t:
     q, kv_data, qo_indptr, kv_indptr, config = data
     q_seq_len = int(config.get("q_seq_len", 1))
@@ -39,6 +60,8 @@ def custom_kernel(data: input_t) -> output_t:
         raise ValueError("config['num_heads'] does not match q.shape[1]")
     sm_scale = float(config.get("sm_scale", DEFAULT_SM_SCALE))
     kv_mode = config.get("kv_mode", "fp8")
+    if kv_mode == "auto":
+        kv_mode = auto_kv_mode(num_heads, kv_data)
     kv_indices = config.get("kv_indices")
     if q.shape[0] != (kv_indptr.numel() - 1) * q_seq_len:
         raise ValueError("q.shape[0] must equal batch * q_seq_len")

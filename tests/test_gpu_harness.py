@@ -26,6 +26,19 @@ def test_task_shapes_within_north_star_tolerance(cuda, args):
     assert good, msg
 
 
+def test_task_tests_pass_on_the_auto_route(cuda):
+    """kv_mode 'auto' (the MXFP4 cache at 16 heads) passes the task's own
+    check (rtol = atol = 0.1, up to 5 % mismatches) on the four test shapes."""
+    def kernel(data):
+        q, kv_data, qo, kv_indptr, cfg = data
+        return custom_kernel((q, kv_data, qo, kv_indptr, {**cfg, "kv_mode": "auto"}))
+
+    lines = []
+    rc, res = Hn.run("test", Hn.task_cases("test"), kernel=kernel,
+                     log=lambda s: (lines.append(s), print(s, flush=True)))
+    assert rc == 0, "\n".join(lines)
+
+
 def test_short_leaderboard_run(cuda):
     cases = Hn.task_cases("benchmark")[:2]
     rc, res = Hn.run("leaderboard", cases, flush=Hn.L2Flush(64), max_repeats=4,

@@ -40,16 +40,28 @@ def test_plan_covers_every_token_once(cuda, lens, heads, mode):
     assert P["max_items"] == P["layout"]["max_items"] == P["layout"]["target_items"] + B
     target = P["layout"]["plan_target"]
     assert target <= P["layout"]["target_items"] and P["num_items"] <= target + B
-    # B <= 256: the smallest multiple of 64 (>= c0) whose piece count fits
-    # `target` (or the longest sequence); otherwise c0 = max(128, 64 ceil(T / (64 target)))
+    assert P["chunk"] == expected_chunk(lens, target, 128, 0)
+    check_cover(P, lens, indptr)
+
+
+def expected_chunk(lens, target, min_chunk, max_splits):
+    """B <= 256: the smallest multiple of 64 (>= c0) whose piece count fits
+    `target` (or the longest sequence); otherwise c0 = max(min_chunk, 64
+    ceil(T / (64 target)), and with a split cap 64 ceil(ceil(Lmax / 64) /
+    max_splits))."""
     per = -(-sum(lens) // target)
-    c0 = max(128, -(-per // 64) * 64)
+    c0 = max(min_chunk, -(-per // 64) * 64)
+    if max_splits > 0:
+        c0 = max(c0, 64 * -(-(-(-max(lens) // 64)) // max_splits))
     count = lambda c: sum(max(1, -(-L // c)) for L in lens)
-    if B <= 256:
+    if len(lens) <= 256:
         cands = [c for c in range(c0, max(c0, -(-max(lens) // 64) * 64) + 1, 64) if count(c) <= target]
-        assert P["chunk"] == (cands[0] if cands else max(c0, -(-max(lens) // 64) * 64))
-    else:
-        assert P["chunk"] == c0
+        return cands[0] if cands else max(c0, -(-max(lens) // 64) * 64)
+    return c0
+
+
+def check_cover(P, lens, indptr):
+    B = len(lens)
     items, binfo = P["items"].tolist(), P["batch_info"].tolist()
     for b in range(B):
         first, cnt = binfo[b]
@@ -70,3 +82,41 @@ def test_plan_covers_every_token_once(cuda, lens, heads, mode):
         order = sorted(range(B), key=lambda b: binfo[b][0])
         pieces = [-(-lens[b] // binfo[b][1]) for b in order]
         assert all(a >= c for a, c in zip(pieces, pieces[1:]))
+
+
+@pytest.mark.parametrize("mode", ["fp8", "mxfp4"])
+@pytest.mark.parametrize("lens", [[1024] * 256, [8192] * 32, [100] * 4, [1024] * 128, [8192] * 4,
+                                  [20000, 3, 700], [(i * 37) % 2000 + 1 for i in range(300)]])
+def test_fused_plan_on_contiguous_rows(cuda, lens, mode):
+    """The fused entry point on a contiguous 16-head cache (no kv_indices)
+    plans with plan_target_for's contiguous rule (one item per CU below that
+    many sequences, a 1024-token chunk floor from there up, at most 32 pieces
+    per sequence): the plan it
+    leaves in the workspace has that chunk and covers every token once, and
+    the output matches the indexed path over the identity indices (whose plan
+    differs) within the operator's 2e-2 tolerance."""
+    from amd_optimization_challenge_amd import inputs
+
+    print(f"contiguous plan mode={mode} B={len(lens)} T={sum(lens)}", flush=True)
+    B, H = len(lens), 16
+    g = torch.Generator(device=cuda).manual_seed(len(lens) + sum(lens))
+    q = torch.randn((B, H, 576), generator=g, device=cuda).to(torch.bfloat16)
+    kv = torch.randn((sum(lens), 1, 576), generator=g, device=cuda).to(torch.bfloat16)
+    kv_data = inputs.build_kv_data(kv, mode)
+    indptr = torch.zeros(B + 1, dtype=torch.int32)
+    indptr[1:] = torch.cumsum(torch.tensor(lens), 0)
+    kv_indptr = indptr.to(cuda)
+    ws = ops.workspace(B, H, mode, cuda)
+    ws.fill_(0x5A)
+    out = ops.decode_fwd(q, kv_data, kv_indptr, None, 576 ** -0.5, mode, ws=ws)
+    torch.cuda.synchronize()
+    P = ops.read_plan(ws, B, H, mode)
+    target, min_chunk, max_splits = ops.plan_target(B, H, ops.kv_mode_id(mode), ops.cu_count(), contiguous=True)
+    assert P["chunk"] == expected_chunk(lens, target, min_chunk, max_splits)
+    assert max(c for _, c in P["batch_info"].tolist()) <= max_splits
+    assert P["num_items"] <= target + B
+    check_cover(P, lens, indptr)
+    ident = torch.arange(sum(lens), dtype=torch.int32, device=cuda)
+    ref = ops.decode_fwd(q, kv_data, kv_indptr, ident, 576 ** -0.5, mode)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(out.float(), ref.float(), rtol=2e-2, atol=2e-2)
