@@ -669,16 +669,29 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
                                  (uint32_t)e1.x, (uint32_t)e1.y, (uint32_t)e1.z, (uint32_t)e1.w,
                                  (uint32_t)e2.x, (uint32_t)e2.y, (uint32_t)e2.z, (uint32_t)e2.w,
                                  (uint32_t)e3.x, (uint32_t)e3.y, (uint32_t)e3.z, (uint32_t)e3.w};
+        // P of tokens (k, k + 1) as a bf16 pair with E_ref taken off both
+        // exponent fields (16-bit lanes, mod 2^16); block jl then adds e << 7
+        // per half, which is the exact bf16 of P 2^(e - E_ref) while that
+        // stays a normal number.  P <= 2^kRebase and e <= E_ref + kVScaleSpan
+        // keep every sum below 2^15, so a negative 16-bit result means the
+        // scaled P fell below the normal range: it becomes 0.
+        u16x2 pq[8];
+        const u16x2 eoff = (u16x2)(unsigned short)(e_ref << 7);
+#pragma unroll
+        for (int k = 0; k < 16; k += 2) pq[k / 2] = __builtin_bit_cast(u16x2, pack_bf16x2(pv[k], pv[k + 1])) - eoff;
 #pragma unroll
         for (int jl = 0; jl < 4; ++jl) {  // block 4w + jl (dims 32(4w + jl) ..): byte jl
-          int ev[16];
-#pragma unroll
-          for (int k = 0; k < 16; ++k) ev[k] = (int)((ed[k] >> (8 * jl)) & 0xFFu);
           uint32_t bw[8];
 #pragma unroll
-          for (int k = 0; k < 16; k += 2)
-            bw[k / 2] = pack_bf16x2(__builtin_amdgcn_ldexpf(pv[k], ev[k] - e_ref),
-                                    __builtin_amdgcn_ldexpf(pv[k + 1], ev[k + 1] - e_ref));
+          for (int k = 0; k < 16; k += 2) {
+            // byte jl of tokens k and k + 1 into the low bytes of the two halves
+            const uint32_t x = __builtin_amdgcn_perm(ed[k + 1], ed[k], jl | 0x0C00u | ((4u + jl) << 16) | 0x0C000000u);
+            // (e << 7) + P per half in one packed multiply-add (the compiler
+            // would shift and add); its operands and result are plain VGPRs
+            uint32_t y;
+            asm("v_pk_mad_u16 %0, %1, %2, %3" : "=v"(y) : "v"(x), "s"(0x00800080u), "v"(pq[k / 2]));
+            bw[k / 2] = __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(s16x2, y), (s16x2)0));
+          }
           const v8bf b0 = __builtin_bit_cast(v8bf, make_uint4(bw[0], bw[1], bw[2], bw[3]));
           const v8bf b1 = __builtin_bit_cast(v8bf, make_uint4(bw[4], bw[5], bw[6], bw[7]));
 #pragma unroll

@@ -20,12 +20,22 @@ s_nop N counts N + 1 wait states, every other instruction one.
 one wait state (gfx9-family rule for an SALU write of M0 read by an LDS DMA).
 3. No scalar-memory stores, atomics or cache write-backs in any kernel.
 4. No packed-FP32 add/mul/fma (the build disables their formation).
+5. No decode, combine, quant or planner kernel spills to scratch (code-object
+   metadata: private segment size and VGPR spill count 0), except the a16w8
+   variant of the 16-head kernel (two fp8 terms of Q, 80 registers, at two
+   work-groups per CU), which is on no benchmarked route.
+
+``python tests/test_isa_rules.py --resources`` prints the per-kernel register,
+LDS and scratch figures of the built library as a markdown table.
 """
 import os
 import re
 import subprocess
+import sys
+import tempfile
 
 import pytest
+import yaml
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 BUILD = os.path.join(ROOT, "amd_optimization_challenge_amd", "_build")
@@ -244,3 +254,80 @@ def test_m0_rule_checker():
     bad = [ok[0], ok[1], (8, "global_load_lds_dwordx4", "v[2:3], off", None)]
     assert not m0_wait_violations(ok)
     assert m0_wait_violations(bad)
+
+
+def kernel_metadata(obj, tmp):
+    """[{name, vgpr, agpr, sgpr, scratch, vgpr_spill, sgpr_spill, lds}] from
+    the AMDGPU metadata note of the gfx950 code object in a built .o (None
+    for a host-only object)."""
+    fat = os.path.join(tmp, "fat.bin")
+    co = os.path.join(tmp, "dev.co")
+    r = subprocess.run([f"{LLVM}/llvm-objcopy", f"--dump-section=.hip_fatbin={fat}", obj, os.path.join(tmp, "host.o")],
+                       capture_output=True)
+    if r.returncode != 0:
+        if b".hip_fatbin' not found" in r.stderr:
+            return None
+        raise subprocess.CalledProcessError(r.returncode, r.args, r.stdout, r.stderr)
+    subprocess.run([f"{LLVM}/clang-offload-bundler", "--type=o", "--targets=hipv4-amdgcn-amd-amdhsa--gfx950",
+                    f"--input={fat}", f"--output={co}", "--unbundle"], check=True, capture_output=True)
+    txt = subprocess.run([f"{LLVM}/llvm-readobj", "--notes", co], check=True, capture_output=True, text=True).stdout
+    doc = txt.split("AMDGPU Metadata: ", 1)[1]
+    doc = doc[:doc.index("\n...")] if "\n..." in doc else doc
+    out = []
+    for k in yaml.safe_load(doc)["amdhsa.kernels"]:
+        out.append(dict(name=k[".name"], vgpr=k[".vgpr_count"], agpr=k.get(".agpr_count", 0), sgpr=k[".sgpr_count"],
+                        scratch=k[".private_segment_fixed_size"], vgpr_spill=k[".vgpr_spill_count"],
+                        sgpr_spill=k[".sgpr_spill_count"], lds=k[".group_segment_fixed_size"]))
+    return out
+
+
+SCRATCH_CHECKED = ("decode.o", "decode_h128.o", "quant.o", "noalloc.o")
+A16W8 = re.compile(r"decode_h16_kernelILi0ELi0ELb[01]ELi2E")
+
+
+def test_no_scratch_in_the_operator_kernels(tmp_path):
+    if not os.path.isdir(BUILD) or not os.path.exists(os.path.join(BUILD, "decode.o")):
+        pytest.skip("library not built (run __graft_entry__.build())")
+    if not os.path.exists(f"{LLVM}/llvm-readobj"):
+        pytest.skip("ROCm LLVM tools not found")
+    bad, seen = [], 0
+    for obj in SCRATCH_CHECKED:
+        path = os.path.join(BUILD, obj)
+        if not os.path.exists(path):
+            continue
+        d = tmp_path / obj[:-2]
+        d.mkdir()
+        for k in kernel_metadata(path, str(d)) or []:
+            seen += 1
+            if A16W8.search(k["name"]):
+                continue
+            if k["scratch"] or k["vgpr_spill"]:
+                bad.append(f"{obj} {k['name']}: {k['scratch']} B scratch, {k['vgpr_spill']} VGPRs spilled")
+    assert seen >= 20, seen
+    assert not bad, "\n".join(bad)
+
+
+def resources_markdown():
+    import shutil
+
+    rows = []
+    for obj in sorted(f for f in os.listdir(BUILD) if f.endswith(".o")):
+        with tempfile.TemporaryDirectory() as d:
+            for k in kernel_metadata(os.path.join(BUILD, obj), d) or []:
+                name = k["name"]
+                if shutil.which("c++filt"):
+                    name = subprocess.run(["c++filt", name], capture_output=True, text=True).stdout.strip()
+                rows.append((obj, name, k))
+    lines = ["| object | kernel | VGPR | AGPR | SGPR | scratch B/lane | VGPR spills | SGPR spills | LDS B |",
+             "|---|---|---|---|---|---|---|---|---|"]
+    for obj, name, k in rows:
+        lines.append(f"| {obj} | `{name}` | {k['vgpr']} | {k['agpr']} | {k['sgpr']} | {k['scratch']} | "
+                     f"{k['vgpr_spill']} | {k['sgpr_spill']} | {k['lds']} |")
+    return "\n".join(lines)
+
+
+if __name__ == "__main__":
+    if sys.argv[1:] == ["--resources"]:
+        print(resources_markdown())
+    else:
+        sys.exit("usage: python tests/test_isa_rules.py --resources")
