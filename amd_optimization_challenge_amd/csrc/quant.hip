@@ -388,10 +388,41 @@ __device__ __forceinline__ void build_plan_wave(const int32_t* __restrict__ kv_i
   const int n_items = __builtin_amdgcn_readlane(x, 63);
   const int first = __builtin_amdgcn_ds_bpermute(rank << 2, x - by_rank);
   if (act) {
-    int4* items = reinterpret_cast<int4*>(plan + kPlanHeader);
     int2* binfo = reinterpret_cast<int2*>(plan + kPlanHeader + 4 * max_items);
     binfo[lane] = make_int2(first, nb);
-    emit_pieces(items, lane, s0, L, nb, first);
+  }
+  // items in parallel, lane i writing items i, i + 64, ...: in rank order the
+  // inclusive scan x is non-decreasing (ranks past the batch add 0), so item
+  // i belongs to rank c = #{r : x_r <= i}, found by a 6-step binary search
+  // over x (ds_bpermute); that rank's row, start, length and count come the
+  // same way.  Piece j of [s0, s0 + L) in nb pieces starts at s0 + j q +
+  // floor(j r / nb) (q = L / nb, r = L % nb), the bounds emit_pieces' running
+  // remainder gives; j r < nb^2 stays in 32 bits.
+  {
+    int4* items = reinterpret_cast<int4*>(plan + kPlanHeader);
+    const int seq_r = __builtin_amdgcn_ds_permute(rank << 2, lane);
+    const int s0_r = __builtin_amdgcn_ds_permute(rank << 2, s0);
+    const int len_r = __builtin_amdgcn_ds_permute(rank << 2, L);
+    const int first_r = x - by_rank;
+    for (int base = 0; base < n_items; base += 64) {
+      const int i = base + lane;
+      int c = 0;
+#pragma unroll
+      for (int step = 32; step >= 1; step >>= 1)
+        if (__builtin_amdgcn_ds_bpermute((c + step - 1) << 2, x) <= i) c += step;
+      const int bi = __builtin_amdgcn_ds_bpermute(c << 2, seq_r);
+      const int sb = __builtin_amdgcn_ds_bpermute(c << 2, s0_r);
+      const int lb = __builtin_amdgcn_ds_bpermute(c << 2, len_r);
+      const int nbb = __builtin_amdgcn_ds_bpermute(c << 2, by_rank);
+      const int fb = __builtin_amdgcn_ds_bpermute(c << 2, first_r);
+      if (i < n_items) {
+        const unsigned j = (unsigned)(i - fb), n = (unsigned)nbb;
+        const unsigned q = (unsigned)lb / n, r = (unsigned)lb - q * n;
+        const int t0 = sb + (int)(j * q + (j * r) / n);
+        const int t1 = sb + (int)((j + 1) * q + ((j + 1) * r) / n);
+        items[i] = make_int4(bi, t0, t1, nbb > 1 ? i : -1);
+      }
+    }
   }
   if (lane == 0) {
     plan[0] = n_items;
