@@ -44,6 +44,7 @@ SIGNATURES = {
     "mla_decode_fwd_noalloc": (_I, [_P, _P, _L, _P, _L, _P, _L, _P, _P, _P, _I, _I, _I, _F, _I, _P, _P, _P]),
     "mla_noalloc_scratch_bytes": (_L, []),
     "mla_probe_gather": (_I, [_I, _I, _I, _I, _I, _P, _L, _P, _L, _P, _L, _P, _L, _P, _P]),
+    "mla_probe_lds": (_I, [_I, _I, _I, _P, _P, _P]),
 }
 
 

@@ -209,6 +209,72 @@ __global__ __launch_bounds__(256) void probe_stream_kernel(const uint4* __restri
   if (acc == 0x9E3779B9u) sink[threadIdx.x] = acc;
 }
 
+// ---------------------------------------------------------------------------
+// LDS read-pattern probe: each wave repeats 8 LDS reads of one pattern `iters`
+// times and records its shader-clock cycles per read instruction, so a bank
+// counter pass (SQ_LDS_BANK_CONFLICT, SQ_ACTIVE_INST_LDS) over these kernels
+// shows what the counters read for reads that cannot conflict beside the
+// decode kernels' own patterns:
+//   0  ds_read_b128, lane l at 16 l (+1 KiB per read): contiguous, no conflict
+//   1  ds_read_b128, the 128-head fp8 K fragment reads: 608-byte rows, 16-byte
+//      chunk c of row r at 16 (c ^ ((r >> 2) & 7)) (c < 32), lane (l32, hh)
+//      reads row l32, chunks 4 ks + 2 hh + j (ks < 4, j < 2)
+//   2  ds_read_b64_tr_b8, lane l at 8 l (+512 B per read): contiguous
+//   3  ds_read_b64_tr_b8, the 128-head V^T reads: lane (G, m, oo) reads row
+//      T0 + 16 cc, chunk 2 dt + (G & 1), byte 8 oo, T0 = 8 (m >> 2) + 4 hh + (m & 3)
+//   4  ds_read_b128, lane l at 512 l mod 32 KiB: every lane on the same banks
+// ---------------------------------------------------------------------------
+constexpr int kLdsProbeBytes = 64 * 608;
+
+__device__ __forceinline__ uint32_t k608(int r, int c) {
+  const int x = (r >> 2) & 7;
+  return (uint32_t)(r * 608 + 16 * (c < 32 ? (c ^ x) : 32 + ((c - 32) ^ (x & 3))));
+}
+
+template <int PAT>
+__global__ __launch_bounds__(256) void probe_lds_kernel(int iters, float* __restrict__ cycles,
+                                                        uint32_t* __restrict__ sink) {
+  __shared__ __attribute__((aligned(16))) uint8_t buf[kLdsProbeBytes];
+  for (int i = threadIdx.x; i < kLdsProbeBytes / 16; i += 256)
+    reinterpret_cast<uint4*>(buf)[i] = make_uint4(i, i * 3u, i * 5u, i * 7u);
+  __syncthreads();
+  const int lane = threadIdx.x & 63, l32 = lane & 31, hh = lane >> 5;
+  const uint32_t base = (uint32_t)(uintptr_t)buf;
+  uint32_t off[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    if constexpr (PAT == 0) off[i] = 16 * lane + 1024 * i;
+    else if constexpr (PAT == 1) off[i] = k608(l32, 4 * (i >> 1) + 2 * hh + (i & 1));
+    else if constexpr (PAT == 2) off[i] = 8 * lane + 512 * i;
+    else if constexpr (PAT == 3) {
+      const int G = lane >> 4, m = (lane & 15) >> 1, oo = lane & 1;
+      const int T0 = 8 * (m >> 2) + 4 * hh + (m & 3);
+      off[i] = k608(T0 + 16 * (i & 3), 2 * (i >> 2) + (G & 1)) + 8 * oo;
+    } else {
+      off[i] = (512 * lane + 16 * i) % 32768;
+    }
+  }
+  uint32_t acc = 0;
+  const uint64_t t0 = __builtin_amdgcn_s_memtime();
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) asm volatile("" : "+v"(off[i]));  // no hoisting out of the loop
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if constexpr (PAT == 2 || PAT == 3) {
+        const v2i v = lds_read_tr8(base + off[i]);
+        acc ^= (uint32_t)v[0] ^ (uint32_t)v[1];
+      } else {
+        const uint4 v = *reinterpret_cast<const uint4*>(buf + off[i]);
+        acc ^= v.x ^ v.w;
+      }
+    }
+  }
+  const uint64_t t1 = __builtin_amdgcn_s_memtime();
+  if (lane == 0) cycles[blockIdx.x * 4 + (threadIdx.x >> 6)] = (float)(t1 - t0) / (8.0f * (float)iters);
+  if (acc == 0x9E3779B9u) sink[threadIdx.x] = acc;
+}
+
 template <int LAYOUT, int METHOD, int NW, int S>
 hipError_t launch_dma(int grid, const uint8_t* rows, int64_t rs, const uint8_t* sc, int64_t ss, const uint8_t* v,
                       int64_t vs, const int32_t* idx, int ntiles, uint32_t* sink, hipStream_t st) {
@@ -228,6 +294,24 @@ hipError_t launch_dma(int grid, const uint8_t* rows, int64_t rs, const uint8_t* 
 using namespace mla;
 
 extern "C" {
+
+int mla_probe_lds(int pattern, int iters, int groups, float* cycles, void* sink, void* stream) {
+  if (iters < 1 || groups < 1 || groups > 65535) return set_error(MLA_ERR_INVALID_ARGUMENT, "iters, groups >= 1");
+  if (!cycles || !sink) return set_error(MLA_ERR_INVALID_ARGUMENT, "null cycles or sink");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  uint32_t* sk = static_cast<uint32_t*>(sink);
+  switch (pattern) {
+    case 0: hipLaunchKernelGGL(probe_lds_kernel<0>, dim3(groups), dim3(256), 0, st, iters, cycles, sk); break;
+    case 1: hipLaunchKernelGGL(probe_lds_kernel<1>, dim3(groups), dim3(256), 0, st, iters, cycles, sk); break;
+    case 2: hipLaunchKernelGGL(probe_lds_kernel<2>, dim3(groups), dim3(256), 0, st, iters, cycles, sk); break;
+    case 3: hipLaunchKernelGGL(probe_lds_kernel<3>, dim3(groups), dim3(256), 0, st, iters, cycles, sk); break;
+    case 4: hipLaunchKernelGGL(probe_lds_kernel<4>, dim3(groups), dim3(256), 0, st, iters, cycles, sk); break;
+    default: return set_error(MLA_ERR_INVALID_ARGUMENT, "pattern must be 0..4");
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return set_error(MLA_ERR_HIP, "probe launch: %s", hipGetErrorString(e));
+  return MLA_OK;
+}
 
 int mla_probe_gather(int layout, int method, int waves, int stages, int groups, const void* rows,
                      int64_t row_stride, const void* scales, int64_t scale_stride, const void* v_rows,

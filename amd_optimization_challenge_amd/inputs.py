@@ -86,6 +86,28 @@ def build_kv_data(kv: torch.Tensor, kv_mode: str) -> dict:
     return kv_data
 
 
+def mxfp4_in_row(kv_data: dict, row_bytes: int = 320) -> dict:
+    """The same caches with each token's 18 e8m0 bytes stored in its packed
+    row: one [T, row_bytes] uint8 buffer, packed e2m1 at bytes 0..287, scales at
+    288..305, zero padding after; kv_data["mxfp4"] becomes the two strided
+    views (row stride row_bytes for both), which every kv_mode reading the
+    mxfp4 cache accepts.  A random token then costs one 320-byte row in HBM
+    instead of a 288-byte row and an 18-byte row (each a 128-byte line or more)."""
+    from . import ops
+
+    packed, scales = kv_data["mxfp4"]
+    p = ops.as_bytes(packed).reshape(-1, QK_DIM // 2)
+    sc = ops.as_bytes(scales).reshape(p.shape[0], -1)[:, :QK_DIM // 32]
+    if row_bytes < QK_DIM // 2 + QK_DIM // 32 or row_bytes % 16:
+        raise ValueError("row_bytes must be a multiple of 16 and hold 306 bytes")
+    buf = torch.zeros((p.shape[0], row_bytes), dtype=torch.uint8, device=p.device)
+    buf[:, :QK_DIM // 2] = p
+    buf[:, QK_DIM // 2:QK_DIM // 2 + QK_DIM // 32] = sc
+    out = dict(kv_data)
+    out["mxfp4"] = (buf[:, :QK_DIM // 2], buf[:, QK_DIM // 2:QK_DIM // 2 + QK_DIM // 32])
+    return out
+
+
 def make_config(batch, num_heads, kv_lens_total, kv_mode, sm_scale, kv_indices, kv_seq_len):
     return {
         "batch_size": batch,

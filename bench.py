@@ -44,18 +44,24 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
+# the sources that decide what a decode launch does: its kernels, the planner
+# that cuts its items, and the entry points that set it up (not the probes,
+# self-tests or the neighbouring steps)
+DECODE_SOURCES = ("abi.hip", "decode.hip", "decode_h128.hip", "quant.hip", "mla_common.hpp", "mla_internal.hpp")
+
+
 def source_digest():
-    """First 16 hex digits of the SHA-256 over the library's HIP sources (name +
-    bytes, sorted): identifies the kernels a counter profile was taken on."""
+    """First 16 hex digits of the SHA-256 over the decode path's sources
+    (DECODE_SOURCES, name + bytes, in that order): identifies the kernels a
+    counter profile was taken on."""
     import hashlib
 
     d = hashlib.sha256()
     csrc = os.path.join(ROOT, "amd_optimization_challenge_amd", "csrc")
-    for name in sorted(os.listdir(csrc)):
-        if name.endswith((".hip", ".hpp")):
-            d.update(name.encode())
-            with open(os.path.join(csrc, name), "rb") as f:
-                d.update(f.read())
+    for name in DECODE_SOURCES:
+        d.update(name.encode())
+        with open(os.path.join(csrc, name), "rb") as f:
+            d.update(f.read())
     return d.hexdigest()[:16]
 
 
@@ -221,17 +227,42 @@ def time_config(cid, steps, warmup, flush_buf, probe=True):
     ncopy = min(64, max(2, -(-(512 << 20) // cache_bytes) + 1))  # config 1's 0.6 MB cache stays warm
     copies = make_copies(kv_data, ncopy)
     args = (kv_indptr, cfg["kv_indices"], H, cfg["sm_scale"], mode, ws, out)
-    for i in range(ncopy):  # warm-up: every copy once
-        ops.decode(qf8, qsc, copies[i], *args)
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    e0.record()
-    for i in range(steps):
-        ops.decode(qf8, qsc, copies[i % ncopy], *args)
-    e1.record()
+
+    def time_decode(cs):
+        """us per launch: `steps` back-to-back launches captured in one HIP
+        graph, one event pair around a replay.  Eager launches from Python
+        arrive slower than a 10-us kernel runs (the GPU would wait on the
+        host), and an event pair per launch adds its own barrier, several us,
+        to every launch.  Each launch's share includes the boundary to the next
+        kernel.  The decode path records no memset and allocates nothing."""
+        for c in cs:  # warm-up: every copy once, eagerly
+            ops.decode(qf8, qsc, c, *args)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(steps):
+                ops.decode(qf8, qsc, cs[i % len(cs)], *args)
+        g.replay()  # warm-up replay
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        del g
+        return e0.elapsed_time(e1) * 1e3 / steps
+
+    dec_mean = time_decode(copies)
     ops.combine(B, H, ws, out)
     torch.cuda.synchronize()
-    dec_us = [e0.elapsed_time(e1) * 1e3 / steps]
+    inrow = None
+    if mode in ("mxfp4", "mxfp4k_fp8v"):
+        # the same decode over caches with the scales inside each 320-B row
+        rc = [inputs.mxfp4_in_row(c) for c in copies]
+        inrow = time_decode(rc)
+        del rc
+        ops.decode(qf8, qsc, kv_data, *args)  # leave `out` from the separate-array caches
+        ops.combine(B, H, ws, out)
 
     # the gather ceiling of this config: the probe's variants for its cache
     # layout over the same rows (kv_indices, whole 64-token tiles), same copies
@@ -256,7 +287,6 @@ def time_config(cid, steps, warmup, flush_buf, probe=True):
 
     call_bytes, dec_bytes, flops = algorithmic(spec, T)
     call_mean = sum(call_us) / len(call_us)
-    dec_mean = sum(dec_us) / len(dec_us)
     res = {
         "name": spec["name"], "batch": B, "num_heads": H, "kv_mode": mode, "total_kv": T,
         "us_per_call_mean": round(call_mean, 3), "us_per_call_median": round(sorted(call_us)[len(call_us) // 2], 3),
@@ -271,6 +301,9 @@ def time_config(cid, steps, warmup, flush_buf, probe=True):
     if gather is not None:
         res["gather_ceiling"] = gather
         res["frac_of_gather_ceiling"] = round(gather["us"] / dec_mean, 4)
+    if inrow is not None:
+        res["in_row_scales"] = {"us_decode_kernel_mean": round(inrow, 3),
+                                "decode_hbm_GBs": round(dec_bytes / (inrow * 1e-6) / 1e9, 1)}
     log(f"[bench] config {cid}: {res['us_per_call_mean']} us/call, decode {res['us_decode_kernel_mean']} us "
         f"({res['decode_hbm_GBs']} GB/s, {100 * res['decode_hbm_frac']:.1f}% HBM)"
         + (f", gather ceiling {gather['us']} us ({gather['GBs']} GB/s)" if gather else ""))
@@ -374,7 +407,8 @@ def cpu_baseline(cid, data, budget_s):
 def profile_decode(cids, reps):
     """Counter-collection driver (run under rocprofv3 --pmc): one 256 MiB copy
     (the FETCH_SIZE / WRITE_SIZE calibration kernel), then per config one Q
-    quant + plan and `reps` decode launches, each after a 512 MiB flush."""
+    quant + plan and `reps` decode launches, each after a 512 MiB flush; for
+    the mxfp4 configs `reps` more over the scales stored in each 320-B row."""
     import torch
 
     from amd_optimization_challenge_amd import inputs, ops
@@ -403,8 +437,47 @@ def profile_decode(cids, reps):
             ops.decode(qf8, qsc, kv_data, kv_indptr, cfg["kv_indices"], H, cfg["sm_scale"], mode, ws, out)
         torch.cuda.synchronize()
         log(f"[profile] config {cid}: {reps} decode launches done")
+        if mode in ("mxfp4", "mxfp4k_fp8v"):  # then over scales stored in each 320-B row
+            inrow = inputs.mxfp4_in_row(kv_data)
+            for _ in range(reps):
+                flush.zero_()
+                ops.decode(qf8, qsc, inrow, kv_indptr, cfg["kv_indices"], H, cfg["sm_scale"], mode, ws, out)
+            torch.cuda.synchronize()
+            log(f"[profile] config {cid}: {reps} decode launches on in-row scales done")
+            del inrow
         del data, ws, out
         torch.cuda.empty_cache()
+
+
+LDS_PATTERNS = {0: "ds_read_b128 contiguous", 1: "ds_read_b128 128-head fp8 K fragments (608-B rows, key (r>>2)&7)",
+                2: "ds_read_b64_tr_b8 contiguous", 3: "ds_read_b64_tr_b8 128-head V^T (608-B rows, key (r>>2)&7)",
+                4: "ds_read_b128, every lane on the same banks"}
+
+
+def lds_probe(iters=4096, groups=256):
+    """mla_probe_lds over its five read patterns: cycles per wave-level read
+    instruction at 4 waves per CU (one work-group per CU), for the LDS bank
+    counter pass beside the decode kernels."""
+    import ctypes
+
+    import torch
+
+    from amd_optimization_challenge_amd import _lib
+
+    lib = _lib.load()
+    cyc = torch.zeros(4 * groups, dtype=torch.float32, device="cuda")
+    sink = torch.zeros(256, dtype=torch.int32, device="cuda")
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    out = []
+    for pat, name in LDS_PATTERNS.items():
+        for _ in range(2):  # warm-up, then the recorded launch
+            _lib.check(lib.mla_probe_lds(pat, iters, groups, ctypes.c_void_p(cyc.data_ptr()),
+                                         ctypes.c_void_p(sink.data_ptr()), st), "mla_probe_lds")
+        torch.cuda.synchronize()
+        out.append({"pattern": pat, "reads": name, "cycles_per_instruction": round(float(cyc.mean()), 2)})
+        log(f"[lds] pattern {pat}: {out[-1]['cycles_per_instruction']} cycles per read instruction ({name})")
+    return {"metric": "LDS read patterns: shader-clock cycles per wave-level read instruction", "iters": iters,
+            "groups": groups, "waves_per_group": 4, "results": out}
 
 
 def bench_append(n_tokens, steps, warmup):
@@ -507,6 +580,8 @@ def main(argv=None):
                     help="time the KV-cache append writer at this many tokens instead (own JSON line)")
     ap.add_argument("--neighbours", action="store_true",
                     help="time W_UK absorption and v_up_proj (+fp8) instead (own JSON line)")
+    ap.add_argument("--lds-probe", action="store_true",
+                    help="time the LDS read-pattern probe instead (own JSON line)")
     ap.add_argument("--profile-decode", action="store_true",
                     help="decode-only launches for counter collection (no JSON line)")
     args = ap.parse_args(argv)
@@ -524,6 +599,9 @@ def main(argv=None):
         return 0
     if args.neighbours:
         print(json.dumps(bench_neighbours(args.steps, args.warmup)), flush=True)
+        return 0
+    if args.lds_probe:
+        print(json.dumps(lds_probe()), flush=True)
         return 0
     if args.gather_probe:
         print(json.dumps(gather_probe_sweep(max(args.steps, 5))), flush=True)

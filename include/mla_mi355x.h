@@ -266,6 +266,18 @@ int mla_probe_gather(int layout, int method, int waves, int stages, int groups, 
                      void* stream);
 
 /*
+ * LDS read-pattern probe (no counterpart in the reference): `groups`
+ * work-groups of 4 waves each repeat 8 LDS reads of one pattern `iters` times;
+ * cycles[4 g + w] gets wave w of group g's shader-clock cycles per read
+ * instruction.  Patterns (csrc/probe.hip): 0 contiguous ds_read_b128, 1 the
+ * 128-head fp8 K fragment reads, 2 contiguous ds_read_b64_tr_b8, 3 the
+ * 128-head V^T transpose reads, 4 ds_read_b128 with every lane on the same
+ * banks.  For bank-counter passes beside the decode kernels.  cycles: 4 x
+ * groups floats; sink: 1 KiB of device memory.
+ */
+int mla_probe_lds(int pattern, int iters, int groups, float* cycles, void* sink, void* stream);
+
+/*
  * Diagnostics (no counterpart in the reference): runs one wave of a built-in
  * check that pins an MFMA operand/accumulator layout or a conversion the
  * kernels rely on.  `in`/`out` are small device buffers whose layout per

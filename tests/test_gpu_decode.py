@@ -121,6 +121,26 @@ def test_mxfp4_scale_row_stride(cuda, heads, mode):
         assert torch.equal(got, base), cols
 
 
+@pytest.mark.parametrize("heads,mode", [(16, "mxfp4"), (16, "mxfp4k_fp8v"), (128, "mxfp4k_fp8v")])
+def test_mxfp4_scales_in_row(cuda, heads, mode):
+    """Scales stored inside each 320-byte packed row (inputs.mxfp4_in_row:
+    both caches strided views of one buffer) give the separate-array result
+    bit for bit, and so does the whole operator on that layout."""
+    from amd_optimization_challenge_amd import inputs
+
+    print(f"in-row scales H={heads} mode={mode}", flush=True)
+    q, kv, indptr, idx, qb, caches = host_case([700, 129, 64, 1], heads, mode, seed=31, permute=True)
+    data = device_data(q, kv, indptr, idx, caches, mode, 1 / math.sqrt(192))
+    base = custom_kernel(data).clone()
+    qd, kv_data, qo, kv_indptr, cfg = data
+    inrow = inputs.mxfp4_in_row(kv_data)
+    k, s = inrow["mxfp4"]
+    assert k.stride(0) == s.stride(0) == 320 and s.data_ptr() == k.data_ptr() + 288
+    got = custom_kernel((qd, inrow, qo, kv_indptr, cfg))
+    torch.cuda.synchronize()
+    assert torch.equal(got, base)
+
+
 @pytest.mark.parametrize("heads,mode", [(16, "fp8"), (128, "fp8"), (16, "mxfp4"), (128, "mxfp4k_fp8v")])
 def test_cache_permutation_is_exact(cuda, heads, mode):
     # moving cache rows together with kv_indices leaves the output bit-identical
