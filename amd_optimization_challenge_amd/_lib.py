@@ -38,6 +38,7 @@ SIGNATURES = {
     "mla_combine": (_I, [_I, _I, _P, _L, _P, _P, _P]),
     "mla_decode_fwd": (_I, [_P, _P, _L, _P, _L, _P, _L, _P, _P, _P, _I, _I, _I, _F, _I, _P, _L, _P, _P, _P]),
     "mla_decode_fwd_a16w8": (_I, [_P, _P, _L, _P, _L, _P, _L, _P, _P, _P, _I, _I, _I, _F, _I, _P, _L, _P, _P, _P]),
+    "mla_decode_fwd_rowq": (_I, [_P, _P, _L, _P, _L, _P, _L, _P, _P, _P, _I, _I, _I, _F, _I, _P, _L, _P, _P, _P]),
     "mla_absorb_q": (_I, [_P, _P, _P, _I, _I, _P, _P]),
     "mla_v_up_proj": (_I, [_P, _P, _I, _I, _P, _P, _P, _P, _L, _P]),
     "mla_selftest": (_I, [_I, _P, _P, _P]),

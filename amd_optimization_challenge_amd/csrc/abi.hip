@@ -202,6 +202,12 @@ int decode_params(const void* q_fp8, const float* q_scale, const void* k_cache, 
   p->q_bf16 = nullptr;
   p->q_partials = nullptr;
   p->q_nparts = 0;
+  p->q_per_row = 0;
+  p->plan_here = 0;
+  p->plan_qlen = 1;
+  p->plan_target = 0;
+  p->plan_min_chunk = kPlanMinChunk;
+  p->plan_max_splits = 0;
   p->sm_scale = sm_scale;
   p->batch = batch;
   p->num_heads = num_heads;
@@ -355,7 +361,7 @@ int mla_decode(const void* q_fp8, const float* q_scale, const void* k_cache, int
                void* out_bf16, float* lse_out, void* stream) {
   if (kv_mode == MLA_KV_BF16)
     return set_error(MLA_ERR_UNSUPPORTED, "the bf16 cache takes bf16 Q: use mla_decode_fwd (kv_mode bf16)");
-  DecodeParams p;
+  DecodeParams p{};
   WsLayout L;
   int rc = decode_params(q_fp8, q_scale, k_cache, k_row_stride, k_scales, k_scale_stride, v_cache,
                          v_row_stride, kv_scale, kv_indptr, kv_indices, batch, num_heads, sm_scale,
@@ -411,7 +417,7 @@ int mla_decode_fwd(const void* q_bf16, const void* k_cache, int64_t k_row_stride
                 (long long)workspace_bytes);
   uint8_t* q_fp8 = reinterpret_cast<uint8_t*>(ws + L0.qfp8_off);
   float* q_scale = reinterpret_cast<float*>(ws + L0.quant_off + 4096);
-  DecodeParams p;
+  DecodeParams p{};
   WsLayout L;
   rc = decode_params(q_fp8, q_scale, k_cache, k_row_stride, k_scales, k_scale_stride, v_cache,
                      v_row_stride, kv_scale, kv_indptr, kv_indices, batch, num_heads, sm_scale, kv_mode,
@@ -474,7 +480,7 @@ int mla_decode_fwd_a16w8(const void* q_bf16, const void* k_cache, int64_t k_row_
     return set_error(MLA_ERR_WORKSPACE_TOO_SMALL, "workspace needs %lld bytes (got %lld)", (long long)L0.total,
                      (long long)workspace_bytes);
   char* ws = static_cast<char*>(workspace);
-  DecodeParams p;
+  DecodeParams p{};
   WsLayout L;
   // the fp8 Q slots of the workspace are not read on this route
   rc = decode_params(ws + L0.qfp8_off, reinterpret_cast<const float*>(ws + L0.quant_off + 4096), k_cache,
@@ -489,6 +495,61 @@ int mla_decode_fwd_a16w8(const void* q_bf16, const void* k_cache, int64_t k_row_
   if (e != hipSuccess) return hip_fail(e, "plan launch");
   p.q_bf16 = static_cast<const uint16_t*>(q_bf16);  // no partials: each work-group scales its own Q rows
   e = launch_decode(p, kv_mode, L.max_items, s);
+  if (e != hipSuccess) return hip_fail(e, "decode launch");
+  e = launch_combine(p, s);
+  if (e != hipSuccess) return hip_fail(e, "combine launch");
+  return MLA_OK;
+}
+
+int mla_decode_fwd_rowq(const void* q_bf16, const void* k_cache, int64_t k_row_stride, const void* k_scales,
+                        int64_t k_scale_stride, const void* v_cache, int64_t v_row_stride,
+                        const float* kv_scale, const int32_t* kv_indptr, const int32_t* kv_indices, int batch,
+                        int q_seq_len, int num_heads, float sm_scale, int kv_mode, void* workspace,
+                        int64_t workspace_bytes, void* out_bf16, float* lse_out, void* stream) {
+  if (num_heads != 16 || (kv_mode != MLA_KV_FP8 && kv_mode != MLA_KV_MXFP4))
+    return set_error(MLA_ERR_UNSUPPORTED,
+                     "the per-row Q route takes 16 heads and the fp8 or mxfp4 cache (got %d, kv_mode %d)", num_heads,
+                     kv_mode);
+  if (!q_bf16 || !aligned(q_bf16, 16)) return set_error(MLA_ERR_INVALID_ARGUMENT, "q must be non-null and 16-byte aligned");
+  if (!workspace) return set_error(MLA_ERR_INVALID_ARGUMENT, "null workspace");
+  int rc = check_shape(batch, num_heads, kv_mode);
+  if (rc) return rc;
+  if ((rc = check_qlen(batch, q_seq_len))) return rc;
+  int ncu = 0;
+  if ((rc = cu_count(&ncu))) return rc;
+  WsLayout L0 = workspace_layout(batch, num_heads, kv_mode, ncu);
+  if (workspace_bytes < L0.total)
+    return set_error(MLA_ERR_WORKSPACE_TOO_SMALL, "workspace needs %lld bytes (got %lld)", (long long)L0.total,
+                     (long long)workspace_bytes);
+  char* ws = static_cast<char*>(workspace);
+  DecodeParams p{};
+  WsLayout L;
+  // the fp8 Q slots of the workspace are not read on this route
+  rc = decode_params(ws + L0.qfp8_off, reinterpret_cast<const float*>(ws + L0.quant_off + 4096), k_cache,
+                     k_row_stride, k_scales, k_scale_stride, v_cache, v_row_stride, kv_scale, kv_indptr,
+                     kv_indices, batch, num_heads, sm_scale, kv_mode, workspace, workspace_bytes, out_bf16,
+                     lse_out, &p, &L);
+  if (rc) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const PlanTarget t = plan_target_for(batch, num_heads, kv_mode, ncu, kv_indices == nullptr);
+  p.q_bf16 = static_cast<const uint16_t*>(q_bf16);
+  p.q_per_row = 1;
+  int grid = L.max_items;
+  hipError_t e;
+  if (batch <= 64) {
+    // the decode plans its own work: one launch fewer; at most t.items items
+    // for <= 64 rows (the planner's chunk search keeps the count within the target)
+    p.plan_here = 1;
+    p.plan_qlen = q_seq_len;
+    p.plan_target = t.items;
+    p.plan_min_chunk = t.min_chunk;
+    p.plan_max_splits = t.max_splits;
+    grid = t.items + batch < L.max_items ? t.items + batch : L.max_items;
+  } else {
+    e = launch_plan(kv_indptr, batch, q_seq_len, t, L.max_items, reinterpret_cast<int32_t*>(ws + L.plan_off), s);
+    if (e != hipSuccess) return hip_fail(e, "plan launch");
+  }
+  e = launch_decode(p, kv_mode, grid, s);
   if (e != hipSuccess) return hip_fail(e, "decode launch");
   e = launch_combine(p, s);
   if (e != hipSuccess) return hip_fail(e, "combine launch");

@@ -23,6 +23,7 @@
 #include <type_traits>
 
 #include "mla_internal.hpp"
+#include "mla_plan.hpp"
 
 namespace mla {
 
@@ -157,7 +158,9 @@ constexpr int kVScaleSpan = 31;  // fp4 V: P' = P 2^(e - E_ref) <= 2^(96 + 31) s
 // split here into two fp8 terms at a power-of-two row scale 2^e, hi =
 // e4m3(q 2^-e) and lo = e4m3((q 2^-e - hi) 2^4), and QK runs one MFMA per term
 // (the lo one with B scale 2^-4), about 8 significant bits of Q as bf16 has.
-// 3: bf16, used as it is (a16w16, bf16 K).
+// 3: bf16, used as it is (a16w16, bf16 K).  4: bf16, quantized here per
+// head row (the per-tensor rule with the row as the tensor; fp8 or fp4 K), so
+// no tensor-wide amax pass has to run first.
 template <int KF, int VF, bool IDX, int QM>
 __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_kernel(const DecodeParams p) {
   using C = H16<KF, VF>;
@@ -168,8 +171,25 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
   const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
 
   const int32_t* plan = p.plan;
-  if ((int)blockIdx.x >= plan[0]) return;
-  const int4 it = reinterpret_cast<const int4*>(plan + kPlanHeader)[blockIdx.x];
+  int4 it;
+  if (QM == 4 && p.plan_here) {  // only the per-row Q route plans here
+    // wave 0 plans the (<= 64) rows in registers and takes this work-group's
+    // item; work-group 0 also writes what the combine reads of the plan
+    __shared__ int4 s_item;
+    if ((threadIdx.x >> 6) == 0) {
+      const WavePlan P = plan_wave(p.kv_indptr, p.batch, p.plan_qlen, p.plan_target, p.plan_min_chunk,
+                                   p.plan_max_splits);
+      if (blockIdx.x == 0) plan_wave_write_rows(P, p.batch, p.max_items, const_cast<int32_t*>(plan));
+      const int4 mine = plan_wave_item(P, (int)blockIdx.x);
+      if ((threadIdx.x & 63) == 0) s_item = mine;
+    }
+    __syncthreads();
+    it = s_item;
+    if (it.x < 0) return;  // past the plan's items (block-uniform)
+  } else {
+    if ((int)blockIdx.x >= plan[0]) return;
+    it = reinterpret_cast<const int4*>(plan + kPlanHeader)[blockIdx.x];
+  }
   const int b = it.x, t_beg = it.y, t_end = it.z, slot = it.w;
   const int ntok = t_end - t_beg;
   const int ntiles = (ntok + kTile - 1) / kTile;
@@ -396,6 +416,42 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
       for (int ks = 0; ks < 5; ++ks) asm volatile("" : "+v"(qlo[ks]));
       c = __builtin_amdgcn_ldexpf(1.0f, (int)rmax[16 + l16]) * kvs * p.sm_scale * kLog2e;
       lds_barrier();  // every wave holds its fragments (and its row exponent) before the stage is refilled
+    } else if constexpr (QM == 4) {
+      // per head row: the per-tensor rule with the row as the tensor (|q| max,
+      // bf16 scale amax / 448), every row quantized at its own scale
+      uint8_t* qst = smem + (C::S - 1) * C::STAGE;
+      uint32_t* rmax = reinterpret_cast<uint32_t*>(smem + C::OFF_X);  // [16] row maxima (bf16 bits)
+      if (tid < 16) rmax[tid] = 0;
+      uint4 xv[QNJ];
+#pragma unroll
+      for (int j = 0; j < QNJ; ++j) {
+        const int i = tid + 256 * j;
+        if (i < QNV) xv[j] = *reinterpret_cast<const uint4*>(qst + 16 * i);
+      }
+      lds_barrier();  // rmax zeroed
+#pragma unroll
+      for (int j = 0; j < QNJ; ++j) {
+        const int i = tid + 256 * j;
+        if (i < QNV) {
+          const uint32_t wv[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
+          uint32_t m = 0;
+#pragma unroll
+          for (int k = 0; k < 4; ++k) m = max(m, max(wv[k] & 0x7FFFu, (wv[k] >> 16) & 0x7FFFu));
+          atomicMax(&rmax[i / (kQKDim / 8)], m);
+        }
+      }
+      lds_barrier();  // row maxima complete; every bf16 chunk read before the fp8 rows overwrite them
+#pragma unroll
+      for (int j = 0; j < QNJ; ++j) {
+        const int i = tid + 256 * j;
+        if (i < QNV)
+          *reinterpret_cast<uint2*>(qst + 8 * i) =
+              quant8_fp8(xv[j], make_fp8_quant(fp8_scale_from_amax(rmax[i / (kQKDim / 8)])));
+      }
+      lds_barrier();
+      load_q(qst + l16 * kQKDim);
+      c = fp8_scale_from_amax(rmax[l16]) * (KF == 0 ? kvs : 1.0f) * p.sm_scale * kLog2e;
+      lds_barrier();  // every wave holds its fragments and its row's scale before the stage is refilled
     } else if constexpr (QB) {
       uint8_t* qst = smem + (C::S - 1) * C::STAGE;
       uint32_t* xu = reinterpret_cast<uint32_t*>(smem + C::OFF_X);
@@ -829,6 +885,14 @@ static hipError_t launch_decode_t(const DecodeParams& p, int kv_mode, int grid, 
     if (kv_mode == 3) {  // bf16 cache: bf16 Q, used as it is
       if (!QB) return hipErrorInvalidValue;
       hipLaunchKernelGGL((decode_h16_kernel<2, 3, IDX, 3>), dim3(grid), dim3(256), 0, stream, p);
+      return hipGetLastError();
+    }
+    if (QB && p.q_per_row) {  // bf16 Q quantized per head row here (fp8 or mxfp4 cache)
+      switch (kv_mode) {
+        case 0: hipLaunchKernelGGL((decode_h16_kernel<0, 0, IDX, 4>), dim3(grid), dim3(256), 0, stream, p); break;
+        case 1: hipLaunchKernelGGL((decode_h16_kernel<1, 2, IDX, 4>), dim3(grid), dim3(256), 0, stream, p); break;
+        default: return hipErrorInvalidValue;
+      }
       return hipGetLastError();
     }
     if (QB && p.q_nparts == 0) {  // bf16 Q with no tensor-wide scale: a16w8, fp8 K only

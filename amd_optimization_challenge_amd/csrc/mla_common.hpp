@@ -48,6 +48,17 @@ struct DecodeParams {
   int batch;
   int num_heads;
   int max_items;
+  // 16 heads: q_per_row = bf16 Q quantized per head row in the kernel (no
+  // tensor-wide scale); plan_here = the kernel plans its own work (batch <= 64
+  // query rows, plan_qlen per sequence) with the planner's target, chunk floor
+  // and split cap, and its work-group 0 writes the rows' piece counts and the
+  // header the combine reads (plan then points at writable workspace)
+  int q_per_row;
+  int plan_here;
+  int plan_qlen;
+  int plan_target;
+  int plan_min_chunk;
+  int plan_max_splits;
 };
 
 // ---- vector types ------------------------------------------------------------

@@ -1,0 +1,129 @@
+// The split planner's one-wave form (up to 64 query rows), shared by the
+// planner kernel (which writes every item) and the 16-head decode kernel
+// when it plans its own work (it needs one item; its work-group 0 writes the
+// rows' piece counts and the header the combine reads).  The plan itself is
+// described in quant.hip.
+#pragma once
+
+#include "mla_common.hpp"
+
+namespace mla {
+
+// ceil(total / (64 target)) for total = 64 s1 + s0 (the sums of L >> 6 and of
+// L & 63 over the rows), in 32-bit arithmetic: ceil(total / 64) = s1 +
+// ceil(s0 / 64), and nested ceilings of integer quotients compose.  Valid while
+// the sum of L over all rows stays below 2^37 (s1 < 2^31) and there are fewer
+// than 2^25 rows (s0 < 2^31).
+__device__ __forceinline__ unsigned tiles_per_item(unsigned s1, unsigned s0, int target) {
+  const unsigned t64 = s1 + (s0 + 63u) / 64u;
+  return (t64 + (unsigned)target - 1u) / (unsigned)target;
+}
+
+// first key token and key count of query row r
+__device__ __forceinline__ int row_start(const int32_t* __restrict__ kv_indptr, int r, int qlen) {
+  return kv_indptr[r / qlen];
+}
+__device__ __forceinline__ int row_len(const int32_t* __restrict__ kv_indptr, int r, int qlen) {
+  const int b = r / qlen, i = r - b * qlen;
+  return max(kv_indptr[b + 1] - kv_indptr[b] - (qlen - 1 - i), 0);
+}
+
+// One wave's plan of up to 64 rows, in registers.  Lane b (b < batch) holds
+// row b's first item and piece count; in rank order (lane = rank, rows ranked
+// by piece length, longest first) x is the inclusive item count, and seq_r,
+// s0_r, len_r, nb_r the rank's row, first key, key count and piece count.
+struct WavePlan {
+  int n_items, chunk;
+  int first, nb;
+  int x, nb_r, seq_r, s0_r, len_r;
+  unsigned hi64, lo64;
+};
+
+// every reduction, the binary search and the ordering in registers
+// (shuffles; ds_permute to scatter each row's item count to its rank
+// position and ds_bpermute to gather its first item back): one round trip to
+// kv_indptr and no barriers.  The whole wave must be active.
+__device__ __forceinline__ WavePlan plan_wave(const int32_t* __restrict__ kv_indptr, int batch, int qlen,
+                                              int target_items, int min_chunk, int max_splits) {
+  const int lane = threadIdx.x & 63;
+  const bool act = lane < batch;
+  const int s0 = act ? row_start(kv_indptr, lane, qlen) : 0;
+  const int L = act ? row_len(kv_indptr, lane, qlen) : 0;
+  WavePlan P;
+  P.hi64 = (unsigned)wave_sum(L >> 6);
+  P.lo64 = (unsigned)wave_sum(L & 63);
+  const int lmax = wave_max(L);
+  int lo = max(min_chunk / 64, (int)tiles_per_item(P.hi64, P.lo64, target_items));
+  if (max_splits > 0) lo = max(lo, ((lmax + 63) / 64 + max_splits - 1) / max_splits);
+  int hi = max(lo, (lmax + 63) / 64);
+  const int L64 = (L + 63) >> 6;  // ceil(L / (64 m)) = ceil(L64 / m)
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    const int cnt = wave_sum(act ? (L64 > 0 ? (L64 + mid - 1) / mid : 1) : 0);
+    if (cnt <= target_items) hi = mid;
+    else lo = mid + 1;
+  }
+  P.chunk = lo * 64;
+  P.nb = act ? (L > 0 ? (L64 + lo - 1) / lo : 1) : 0;
+  const int piece = act ? (L > 0 ? (L + P.nb - 1) / P.nb : 0) : -1;
+  // rank by piece length, longest first (ties by index); inactive lanes (piece
+  // -1) never count and rank last.  All 64 lanes are read with constant lane
+  // indices, so the loop unrolls into independent readlanes.
+  int rank = 0;
+#pragma unroll
+  for (int b2 = 0; b2 < 64; ++b2) {
+    const int p2 = __builtin_amdgcn_readlane(piece, b2);
+    rank += (p2 > piece) || (p2 == piece && b2 < lane);
+  }
+  if (!act) rank = lane;
+  // item counts in rank order -> inclusive scan -> each row's first item
+  P.nb_r = __builtin_amdgcn_ds_permute(rank << 2, P.nb);
+  P.x = wave_incl_sum(P.nb_r);
+  P.n_items = __builtin_amdgcn_readlane(P.x, 63);
+  P.first = __builtin_amdgcn_ds_bpermute(rank << 2, P.x - P.nb_r);
+  P.seq_r = __builtin_amdgcn_ds_permute(rank << 2, lane);
+  P.s0_r = __builtin_amdgcn_ds_permute(rank << 2, s0);
+  P.len_r = __builtin_amdgcn_ds_permute(rank << 2, L);
+  return P;
+}
+
+// Item i of the plan as (row, first key, end key, partial slot or -1), for a
+// per-lane i (lanes may ask different items; the whole wave must be active;
+// i >= n_items gives row -1).  In rank order x is non-decreasing (ranks past
+// the batch add 0), so item i belongs to rank c = #{r : x_r <= i}, found by a
+// 6-step binary search over x; piece j of [s0, s0 + L) in n pieces starts at
+// s0 + j q + floor(j r / n) (q = L / n, r = L % n), the bounds a running
+// remainder over the pieces gives; j r < n^2 stays in 32 bits.
+__device__ __forceinline__ int4 plan_wave_item(const WavePlan& P, int i) {
+  int c = 0;
+#pragma unroll
+  for (int step = 32; step >= 1; step >>= 1)
+    if (__builtin_amdgcn_ds_bpermute((c + step - 1) << 2, P.x) <= i) c += step;
+  const int bi = __builtin_amdgcn_ds_bpermute(c << 2, P.seq_r);
+  const int sb = __builtin_amdgcn_ds_bpermute(c << 2, P.s0_r);
+  const int lb = __builtin_amdgcn_ds_bpermute(c << 2, P.len_r);
+  const int nbb = __builtin_amdgcn_ds_bpermute(c << 2, P.nb_r);
+  const int fb = __builtin_amdgcn_ds_bpermute(c << 2, P.x - P.nb_r);
+  if (i >= P.n_items || nbb <= 0) return make_int4(-1, 0, 0, -1);
+  const unsigned j = (unsigned)(i - fb), n = (unsigned)nbb;
+  const unsigned q = (unsigned)lb / n, r = (unsigned)lb - q * n;
+  const int t0 = sb + (int)(j * q + (j * r) / n);
+  const int t1 = sb + (int)((j + 1) * q + ((j + 1) * r) / n);
+  return make_int4(bi, t0, t1, nbb > 1 ? i : -1);
+}
+
+// the rows' (first item, piece count) and the plan header
+__device__ __forceinline__ void plan_wave_write_rows(const WavePlan& P, int batch, int max_items,
+                                                     int32_t* __restrict__ plan) {
+  const int lane = threadIdx.x & 63;
+  if (lane < batch) reinterpret_cast<int2*>(plan + kPlanHeader + 4 * max_items)[lane] = make_int2(P.first, P.nb);
+  if (lane == 0) {
+    plan[0] = P.n_items;
+    plan[1] = P.chunk;
+    plan[2] = (int)(64u * P.hi64 + P.lo64);
+    plan[3] = batch;
+    plan[4] = max_items;
+  }
+}
+
+}  // namespace mla

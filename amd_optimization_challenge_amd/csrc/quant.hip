@@ -11,6 +11,7 @@
 // one thread per 32-element block, 64 B in (4 x 16-byte loads), 16 B + 1 B out.
 // KV-cache append: one lane per 8 elements into both caches at given rows.
 #include "mla_internal.hpp"
+#include "mla_plan.hpp"
 
 namespace mla {
 
@@ -309,25 +310,6 @@ __device__ int block_exscan(int v, int* red, int* total) {
   return base + x - v;
 }
 
-// ceil(total / (64 target)) for total = 64 s1 + s0 (the sums of L >> 6 and of
-// L & 63 over the rows), in 32-bit arithmetic: ceil(total / 64) = s1 +
-// ceil(s0 / 64), and nested ceilings of integer quotients compose.  Valid while
-// the sum of L over all rows stays below 2^37 (s1 < 2^31) and there are fewer
-// than 2^25 rows (s0 < 2^31).
-__device__ __forceinline__ unsigned tiles_per_item(unsigned s1, unsigned s0, int target) {
-  const unsigned t64 = s1 + (s0 + 63u) / 64u;
-  return (t64 + (unsigned)target - 1u) / (unsigned)target;
-}
-
-// first key token and key count of query row r
-__device__ __forceinline__ int row_start(const int32_t* __restrict__ kv_indptr, int r, int qlen) {
-  return kv_indptr[r / qlen];
-}
-__device__ __forceinline__ int row_len(const int32_t* __restrict__ kv_indptr, int r, int qlen) {
-  const int b = r / qlen, i = r - b * qlen;
-  return max(kv_indptr[b + 1] - kv_indptr[b] - (qlen - 1 - i), 0);
-}
-
 // the nb near-equal pieces of [s0, s0 + L): piece i = [s0 + floor(iL/nb),
 // s0 + floor((i+1)L/nb)), computed with one division and a running remainder
 __device__ __forceinline__ void emit_pieces(int4* __restrict__ items, int b, int s0, int L, int nb, int first) {
@@ -345,91 +327,18 @@ __device__ __forceinline__ void emit_pieces(int4* __restrict__ items, int b, int
   }
 }
 
-// Up to 64 rows: one wave plans alone, with every reduction, the binary
-// search and the ordering in registers (shuffles; ds_permute to scatter each
-// row's item count to its rank position and ds_bpermute to gather its first
-// item back), so the plan costs one round trip to kv_indptr and no barriers.
-// Same plan as the block version below.
+// Up to 64 rows: one wave plans alone (mla_plan.hpp) and writes the items in
+// parallel, lane i taking items i, i + 64, ...
 __device__ __forceinline__ void build_plan_wave(const int32_t* __restrict__ kv_indptr, int batch, int qlen,
                                                 int target_items, int min_chunk, int max_splits, int max_items,
                                                 int32_t* __restrict__ plan) {
-  const int lane = threadIdx.x & 63;
-  const bool act = lane < batch;
-  const int s0 = act ? row_start(kv_indptr, lane, qlen) : 0;
-  const int L = act ? row_len(kv_indptr, lane, qlen) : 0;
-  const unsigned hi64 = (unsigned)wave_sum(L >> 6), lo64 = (unsigned)wave_sum(L & 63);
-  const int lmax = wave_max(L);
-  int lo = max(min_chunk / 64, (int)tiles_per_item(hi64, lo64, target_items));
-  if (max_splits > 0) lo = max(lo, ((lmax + 63) / 64 + max_splits - 1) / max_splits);
-  int hi = max(lo, (lmax + 63) / 64);
-  const int L64 = (L + 63) >> 6;  // ceil(L / (64 m)) = ceil(L64 / m)
-  while (lo < hi) {
-    const int mid = (lo + hi) >> 1;
-    const int cnt = wave_sum(act ? (L64 > 0 ? (L64 + mid - 1) / mid : 1) : 0);
-    if (cnt <= target_items) hi = mid;
-    else lo = mid + 1;
-  }
-  const int chunk = lo * 64;
-  const int nb = act ? (L > 0 ? (L64 + lo - 1) / lo : 1) : 0;
-  const int piece = act ? (L > 0 ? (L + nb - 1) / nb : 0) : -1;
-  // rank by piece length, longest first (ties by index); inactive lanes (piece
-  // -1) never count and rank last.  All 64 lanes are read with constant lane
-  // indices, so the loop unrolls into independent readlanes.
-  int rank = 0;
-#pragma unroll
-  for (int b2 = 0; b2 < 64; ++b2) {
-    const int p2 = __builtin_amdgcn_readlane(piece, b2);
-    rank += (p2 > piece) || (p2 == piece && b2 < lane);
-  }
-  if (!act) rank = lane;
-  // item counts in rank order -> exclusive scan -> each row's first item
-  const int by_rank = __builtin_amdgcn_ds_permute(rank << 2, nb);
-  const int x = wave_incl_sum(by_rank);
-  const int n_items = __builtin_amdgcn_readlane(x, 63);
-  const int first = __builtin_amdgcn_ds_bpermute(rank << 2, x - by_rank);
-  if (act) {
-    int2* binfo = reinterpret_cast<int2*>(plan + kPlanHeader + 4 * max_items);
-    binfo[lane] = make_int2(first, nb);
-  }
-  // items in parallel, lane i writing items i, i + 64, ...: in rank order the
-  // inclusive scan x is non-decreasing (ranks past the batch add 0), so item
-  // i belongs to rank c = #{r : x_r <= i}, found by a 6-step binary search
-  // over x (ds_bpermute); that rank's row, start, length and count come the
-  // same way.  Piece j of [s0, s0 + L) in nb pieces starts at s0 + j q +
-  // floor(j r / nb) (q = L / nb, r = L % nb), the bounds emit_pieces' running
-  // remainder gives; j r < nb^2 stays in 32 bits.
-  {
-    int4* items = reinterpret_cast<int4*>(plan + kPlanHeader);
-    const int seq_r = __builtin_amdgcn_ds_permute(rank << 2, lane);
-    const int s0_r = __builtin_amdgcn_ds_permute(rank << 2, s0);
-    const int len_r = __builtin_amdgcn_ds_permute(rank << 2, L);
-    const int first_r = x - by_rank;
-    for (int base = 0; base < n_items; base += 64) {
-      const int i = base + lane;
-      int c = 0;
-#pragma unroll
-      for (int step = 32; step >= 1; step >>= 1)
-        if (__builtin_amdgcn_ds_bpermute((c + step - 1) << 2, x) <= i) c += step;
-      const int bi = __builtin_amdgcn_ds_bpermute(c << 2, seq_r);
-      const int sb = __builtin_amdgcn_ds_bpermute(c << 2, s0_r);
-      const int lb = __builtin_amdgcn_ds_bpermute(c << 2, len_r);
-      const int nbb = __builtin_amdgcn_ds_bpermute(c << 2, by_rank);
-      const int fb = __builtin_amdgcn_ds_bpermute(c << 2, first_r);
-      if (i < n_items) {
-        const unsigned j = (unsigned)(i - fb), n = (unsigned)nbb;
-        const unsigned q = (unsigned)lb / n, r = (unsigned)lb - q * n;
-        const int t0 = sb + (int)(j * q + (j * r) / n);
-        const int t1 = sb + (int)((j + 1) * q + ((j + 1) * r) / n);
-        items[i] = make_int4(bi, t0, t1, nbb > 1 ? i : -1);
-      }
-    }
-  }
-  if (lane == 0) {
-    plan[0] = n_items;
-    plan[1] = chunk;
-    plan[2] = (int)(64u * hi64 + lo64);
-    plan[3] = batch;
-    plan[4] = max_items;
+  const WavePlan P = plan_wave(kv_indptr, batch, qlen, target_items, min_chunk, max_splits);
+  plan_wave_write_rows(P, batch, max_items, plan);
+  int4* items = reinterpret_cast<int4*>(plan + kPlanHeader);
+  for (int base = 0; base < P.n_items; base += 64) {
+    const int i = base + (int)(threadIdx.x & 63);
+    const int4 it = plan_wave_item(P, i);
+    if (i < P.n_items) items[i] = it;
   }
 }
 

@@ -277,7 +277,10 @@ def decode_fwd(q, kv_data, kv_indptr, kv_indices, sm_scale, kv_mode="fp8", out=N
     takes it (caches [pages, page_size, 1, row], kv_indptr over pages,
     kv_indices = page ids, kv_last_page_lens), expanded on the device first.
     q_dtype "bf16": the a16w8 route (``mla_decode_fwd_a16w8``; 16 heads, fp8
-    cache): Q keeps its own precision, no per-tensor quantization.
+    cache): Q keeps its own precision, no per-tensor quantization.  q_dtype
+    "fp8_row" (``mla_decode_fwd_rowq``; 16 heads, fp8 or mxfp4 cache): Q
+    quantized per head row inside the decode, which for up to 64 query rows
+    also plans its own work (two launches per call).
     """
     if int(page_size) != 1:
         if kv_indices is None or kv_last_page_lens is None:
@@ -301,10 +304,12 @@ def decode_fwd(q, kv_data, kv_indptr, kv_indices, sm_scale, kv_mode="fp8", out=N
     if out is None:
         out = torch.empty((batch, num_heads, V_DIM), dtype=torch.bfloat16, device=q.device)
     lse = torch.empty((batch, num_heads), dtype=torch.float32, device=q.device) if return_lse else None
-    if q_dtype not in ("fp8", "bf16"):
-        raise ValueError(f"q_dtype must be 'fp8' (a8w8: per-tensor Q quant) or 'bf16' (a16w8), got {q_dtype!r}")
-    fn, name = ((_lib.load().mla_decode_fwd, "mla_decode_fwd") if q_dtype == "fp8"
-                else (_lib.load().mla_decode_fwd_a16w8, "mla_decode_fwd_a16w8"))
+    routes = {"fp8": "mla_decode_fwd", "bf16": "mla_decode_fwd_a16w8", "fp8_row": "mla_decode_fwd_rowq"}
+    if q_dtype not in routes:
+        raise ValueError(f"q_dtype must be 'fp8' (a8w8: per-tensor Q quant), 'bf16' (a16w8) or 'fp8_row' "
+                         f"(per-row Q quant), got {q_dtype!r}")
+    name = routes[q_dtype]
+    fn = getattr(_lib.load(), name)
     with torch.cuda.device(q.device):
         _lib.check(fn(
             _ptr(q), _ptr(k), ks, _ptr(ksc), kss, _ptr(v), vs, _ptr(sc), _ptr(kv_indptr),

@@ -60,8 +60,12 @@ def custom_kernel(data: input_t) -> output_t:
         raise ValueError("config['num_heads'] does not match q.shape[1]")
     sm_scale = float(config.get("sm_scale", DEFAULT_SM_SCALE))
     kv_mode = config.get("kv_mode", "fp8")
+    q_dtype = config.get("q_dtype", "fp8")
     if kv_mode == "auto":
         kv_mode = auto_kv_mode(num_heads, kv_data)
+        # 16 heads: Q quantized per head row in the decode, which for <= 64
+        # query rows also plans its own work (decode + combine: no amax pass)
+        q_dtype = config.get("q_dtype", "fp8_row" if num_heads == 16 else "fp8")
     kv_indices = config.get("kv_indices")
     if q.shape[0] != (kv_indptr.numel() - 1) * q_seq_len:
         raise ValueError("q.shape[0] must equal batch * q_seq_len")
@@ -71,4 +75,4 @@ def custom_kernel(data: input_t) -> output_t:
     return ops.decode_fwd(q, kv_data, kv_indptr, kv_indices, sm_scale, kv_mode, q_seq_len=q_seq_len,
                           return_lse=bool(config.get("return_lse", False)), page_size=page_size,
                           kv_last_page_lens=config.get("kv_last_page_lens"),
-                          q_dtype=config.get("q_dtype", "fp8"))
+                          q_dtype=q_dtype)

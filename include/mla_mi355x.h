@@ -221,6 +221,24 @@ int mla_decode_fwd_a16w8(const void* q_bf16, const void* k_cache, int64_t k_row_
                          void* out_bf16, float* lse_out, void* stream);
 
 /*
+ * mla_decode_fwd with Q quantized per head row instead of per tensor: each
+ * [576] row of bf16 Q gets the per-tensor rule of quantize_fp8
+ * (TASK/reference.py:76-80) with the row as the tensor, inside the decode
+ * kernel, so no tensor-wide amax pass runs first; for batch <= 64 query rows
+ * the decode kernel also plans its own work, so the call is two launches
+ * (decode, combine).  16 heads, the fp8 or the mxfp4 cache.  It replaces the
+ * reference's small-shape route, which quantizes Q per 32-element MXFP4 block
+ * inside its Triton path for the same reason (mixed-mla/submission.py:321-334);
+ * same arguments as mla_decode_fwd.
+ */
+int mla_decode_fwd_rowq(const void* q_bf16, const void* k_cache, int64_t k_row_stride,
+                        const void* k_scales, int64_t k_scale_stride, const void* v_cache,
+                        int64_t v_row_stride, const float* kv_scale, const int32_t* kv_indptr,
+                        const int32_t* kv_indices, int batch, int q_seq_len, int num_heads,
+                        float sm_scale, int kv_mode, void* workspace, int64_t workspace_bytes,
+                        void* out_bf16, float* lse_out, void* stream);
+
+/*
  * mla_decode_fwd without a caller workspace, for callers that cannot allocate
  * device memory (code under HIP graph capture, tight serving loops, harnesses
  * that forbid hipMalloc).  No counterpart in the reference.  Arguments mean what

@@ -18,6 +18,9 @@ task files):
   mxfp4-mm/submission_v18_custom_fused.py:26-108 (``_mxfp4_quant_op``).
   AITER itself is not vendored (un-pinned HEAD clone, setup.sh:52-61), so the
   restatement there is the anchor.
+* ``quantize_fp8_per_row``     -- quantize_fp8_per_tensor with each row as the
+  tensor (this build's per-row Q route; no reference counterpart at row
+  granularity).
 * ``quantize_fp8_with_scale`` / ``append_kv`` -- the element step of
   TASK/reference.py:79-80 at a given scale, and the row-scatter cache writer
   built from it and ``pack_mxfp4`` (the incremental form of reference.py:318-321).
@@ -44,7 +47,9 @@ HIP kernels and the reference use, so agreement between the two is evidence.
 Parity pins (see tests/test_oracle_*.py):
   fp8 quant   -- exhaustive against torch's own float8_e4m3fn cast (the
                  third-party routine the reference calls), plus closed-form
-                 invariants.
+                 invariants; per row: each row equals the per-tensor result
+                 on that row alone, rows 2^20 apart keep their codes, a row
+                 scaled by a power of two keeps its codes and scales its scale.
   mxfp4 pack  -- exhaustive element encoding against the reference's bit-trick
                  formula (restated in the test), scale-rule known answers,
                  round trip.
@@ -188,6 +193,21 @@ def quantize_fp8_per_tensor(x_bits: np.ndarray) -> tuple[np.ndarray, float]:
     amax_bits = int(mag.max()) if mag.size else 0
     s_bits, scale = fp8_scale_from_amax_bits(amax_bits)
     return quantize_fp8_with_scale(bits, scale), np.float32(scale)
+
+
+def quantize_fp8_per_row(x_bits: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """bf16 bits [..., D] -> (e4m3fn codes, same shape; float32 scales [...]):
+    quantize_fp8_per_tensor (TASK/reference.py:76-80) with each row of D as
+    the tensor.  The reference's small-shape MXFP4 route scales Q per 32-element
+    block for the same reason (no tensor-wide pass, mixed-mla/submission.py:
+    330-334); this build's per-row route keeps the fp8 rule at row granularity."""
+    bits = np.asarray(x_bits, dtype=np.uint16)
+    rows = bits.reshape(-1, bits.shape[-1])
+    codes = np.empty_like(rows, dtype=np.uint8)
+    scales = np.empty(rows.shape[0], dtype=np.float32)
+    for r in range(rows.shape[0]):
+        codes[r], scales[r] = quantize_fp8_per_tensor(rows[r])
+    return codes.reshape(bits.shape), scales.reshape(bits.shape[:-1])
 
 
 def quantize_fp8_with_scale(x_bits: np.ndarray, scale: float) -> np.ndarray:
@@ -462,12 +482,16 @@ def reference_path(q_bits, kv_mode, caches, kv_indptr, kv_indices, sm_scale, thr
     quantize Q (a2) -> dequantize Q and KV -> fp32 attention -> bf16 bits.
     q_dtype "bf16" is the a16w8 route (TASK/reference.py:55-58 Q_DTYPE, the
     bf16-Q paths of mixed-mla/submission.py:414-520): Q enters as its bf16
-    values, unquantized.
+    values, unquantized; "fp8_row" quantizes Q per head row
+    (``quantize_fp8_per_row``).
     ``caches`` = dict(fp8_codes, fp8_scale, fp4_packed, fp4_scales) (numpy).
     Returns (out_bf16_bits [rows,H,512], out_f32[, lse [rows,H] natural log]).
     """
     if q_dtype == "bf16":
         q_deq = bf16_to_f32(np.asarray(q_bits, dtype=np.uint16))
+    elif q_dtype == "fp8_row":
+        qc, qs = quantize_fp8_per_row(q_bits)
+        q_deq = e4m3fn_to_f32(qc) * qs[..., None]
     else:
         qc, qs = quantize_fp8_per_tensor(q_bits)
         q_deq = dequant_fp8(qc, qs)

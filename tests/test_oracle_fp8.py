@@ -116,3 +116,29 @@ def test_quantize_invariants():
     assert list(z) == [0x00, 0x80, 0x00]  # zeros stay zero, -0 keeps its sign
     ref_codes, ref_scale = torch_quantize_fp8(bits_to_torch(zb))  # amax clamped to bf16(1e-12)
     assert s == np.float32(ref_scale) and list(ref_codes) == [0x00, 0x80, 0x00]
+
+
+def test_per_row_quantization_is_per_tensor_on_each_row():
+    """quantize_fp8_per_row: each row equals quantize_fp8_per_tensor on that
+    row alone (the reshape keeps rows whole: a transposed or flattened axis
+    would mix rows); rows 2^20 apart in magnitude keep all their codes, where
+    one tensor-wide scale flushes the small row; a row scaled by a power of
+    two keeps its codes and scales its scale by the same power."""
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn((3, 4, 576), generator=g).to(torch.bfloat16)
+    x[1, 2] *= 2.0 ** -20
+    x[2, 0] *= 2.0 ** 7
+    bits = O.bf16_tensor_bits(x)
+    codes, scales = O.quantize_fp8_per_row(bits)
+    assert codes.shape == bits.shape and scales.shape == (3, 4)
+    for b in range(3):
+        for h in range(4):
+            c, s = O.quantize_fp8_per_tensor(bits[b, h])
+            assert np.array_equal(codes[b, h], c) and scales[b, h] == s
+    small = codes[1, 2]
+    assert np.count_nonzero(small & 0x7F) > 500  # per row: the small row is not flushed
+    whole, _ = O.quantize_fp8_per_tensor(bits)
+    assert np.count_nonzero(whole[1, 2] & 0x7F) < 10  # one tensor-wide scale flushes it
+    y = (x[0, 1].float() * 8.0).to(torch.bfloat16)
+    cy, sy = O.quantize_fp8_per_row(O.bf16_tensor_bits(y)[None])
+    assert np.array_equal(cy[0], codes[0, 1]) and sy[0] == np.float32(8.0) * scales[0, 1]
