@@ -47,7 +47,8 @@ def log(msg):
 # the sources that decide what a decode launch does: its kernels, the planner
 # that cuts its items, and the entry points that set it up (not the probes,
 # self-tests or the neighbouring steps)
-DECODE_SOURCES = ("abi.hip", "decode.hip", "decode_h128.hip", "quant.hip", "mla_common.hpp", "mla_internal.hpp")
+DECODE_SOURCES = ("abi.hip", "decode.hip", "decode_h128.hip", "quant.hip", "mla_common.hpp", "mla_internal.hpp",
+                  "mla_plan.hpp")
 
 
 def source_digest():
