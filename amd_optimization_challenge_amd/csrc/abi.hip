@@ -2,6 +2,7 @@
 // Host code only: argument validation, workspace carve-up, launches.  Nothing
 // here allocates device memory or synchronizes the host.
 #include <stdarg.h>
+#include <stdint.h>
 #include <stdio.h>
 
 #include <mutex>
@@ -182,6 +183,9 @@ int decode_params(const void* q_fp8, const float* q_scale, const void* k_cache, 
   }
   if ((kv_mode == MLA_KV_FP8 || kv_mode == MLA_KV_MXFP4K_FP8V) && !kv_scale)
     return set_error(MLA_ERR_INVALID_ARGUMENT, "fp8 cache needs kv_scale");
+  // the kernels form row offsets as 32 x 32 -> 64-bit products (slot x stride)
+  if (k_row_stride > INT32_MAX || k_scale_stride > INT32_MAX || v_row_stride > INT32_MAX)
+    return set_error(MLA_ERR_INVALID_ARGUMENT, "row strides must be below 2^31 bytes");
   char* ws = static_cast<char*>(workspace);
   p->q_fp8 = static_cast<const uint8_t*>(q_fp8);
   p->q_scale = q_scale;

@@ -238,8 +238,13 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
 #pragma unroll
     for (int k = 0; k < C::NA; ++k) {
       const int u = (w - C::RW0) + C::NRW * k;
-      if (u < C::KW) dma16_to_lds(p.k_cache + (int64_t)sl[k] * p.k_row_stride + co[k], sbase + 1024 * u);
-      else if (u < C::NW) dma16_to_lds(p.v_cache + (int64_t)sl[k] * p.v_row_stride + co[k], sbase + 1024 * u);
+      // slot x stride in one v_mad_u64_u32 (both below 2^31, checked on the host)
+      if (u < C::KW)
+        dma16_to_lds(p.k_cache + ((uint64_t)(uint32_t)sl[k] * (uint32_t)p.k_row_stride + (uint32_t)co[k]),
+                     sbase + 1024 * u);
+      else if (u < C::NW)
+        dma16_to_lds(p.v_cache + ((uint64_t)(uint32_t)sl[k] * (uint32_t)p.v_row_stride + (uint32_t)co[k]),
+                     sbase + 1024 * u);
     }
   };
   // fp4 K scales: the 18 e8m0 bytes of token `lane` of tile t as 5 dwords
@@ -251,7 +256,7 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
   auto issue_scales = [&](int t) __attribute__((always_inline)) {
     if constexpr (KF == 1) {
       if (w < C::SCW) {
-        const uint8_t* srow = p.k_scales + (int64_t)slot_of(t, lane) * p.k_scale_stride;
+        const uint8_t* srow = p.k_scales + (uint64_t)(uint32_t)slot_of(t, lane) * (uint32_t)p.k_scale_stride;
         const uint32_t sb = lds0 + C::OFF_SC + (t % C::S) * C::SCST;
 #pragma unroll
         for (int k = 0; k < (kScWin + C::SCW - 1) / C::SCW; ++k) {
