@@ -240,10 +240,10 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
       const int u = (w - C::RW0) + C::NRW * k;
       // slot x stride in one v_mad_u64_u32 (both below 2^31, checked on the host)
       if (u < C::KW)
-        dma16_to_lds(p.k_cache + ((uint64_t)(uint32_t)sl[k] * (uint32_t)p.k_row_stride + (uint32_t)co[k]),
+        dma16_to_lds_nt(p.k_cache + ((uint64_t)(uint32_t)sl[k] * (uint32_t)p.k_row_stride + (uint32_t)co[k]),
                      sbase + 1024 * u);
       else if (u < C::NW)
-        dma16_to_lds(p.v_cache + ((uint64_t)(uint32_t)sl[k] * (uint32_t)p.v_row_stride + (uint32_t)co[k]),
+        dma16_to_lds_nt(p.v_cache + ((uint64_t)(uint32_t)sl[k] * (uint32_t)p.v_row_stride + (uint32_t)co[k]),
                      sbase + 1024 * u);
     }
   };

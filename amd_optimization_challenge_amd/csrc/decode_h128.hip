@@ -461,9 +461,9 @@ __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams 
       asm volatile("" : "+v"(dmap[k / 2]));
       const uint32_t off = (dmap[k / 2] >> (16 * (k % 2))) & 1023u;
       const uint8_t* src = p.k_cache + ((uint64_t)(uint32_t)sl * (uint32_t)p.k_row_stride + off);
-      uint32_t saved;  // M0 saved and restored, one wait state before the DMA (see dma16_to_lds)
+      uint32_t saved;  // M0 saved and restored, one wait state before the DMA; nt as in dma16_to_lds_nt
       asm volatile("s_mov_b32 %0, m0\n\ts_add_u32 m0, %1, %2\n\ts_mov_b32 %0, %0\n\t"
-                   "global_load_lds_dwordx4 %3, off\n\ts_mov_b32 m0, %0"
+                   "global_load_lds_dwordx4 %3, off nt\n\ts_mov_b32 m0, %0"
                    : "=&s"(saved)
                    : "s"(stage_w), "i"(4096 * k), "v"(src)
                    : "memory", "scc");
@@ -529,7 +529,7 @@ __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams 
                                                     (uint32_t)(256 * ty) + off);
         uint32_t saved;
         asm volatile("s_mov_b32 %0, m0\n\ts_add_u32 m0, %1, %2\n\ts_mov_b32 %0, %0\n\t"
-                     "global_load_lds_dwordx4 %3, off\n\ts_mov_b32 m0, %0"
+                     "global_load_lds_dwordx4 %3, off nt\n\ts_mov_b32 m0, %0"
                      : "=&s"(saved)
                      : "s"(base), "i"(4096 * m), "v"(src)
                      : "memory", "scc");

@@ -230,20 +230,30 @@ __device__ __forceinline__ uint2 quant8_fp8(uint4 v, Fp8Quant q) {
 // which the "s" constraint cannot take.
 #define MLA_LDS_DMA(INSN)                                                                          \
   uint32_t saved;                                                                                  \
-  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_mov_b32 %0, %0\n\t" INSN " %2, off\n\t" \
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_mov_b32 %0, %0\n\t" INSN "\n\t"        \
                "s_mov_b32 m0, %0"                                                                  \
                : "=&s"(saved)                                                                      \
                : "s"(__builtin_amdgcn_readfirstlane(lds_off)), "v"(g)                             \
                : "memory")
 __device__ __forceinline__ void dma16_to_lds(const void* g, uint32_t lds_off) {
-  MLA_LDS_DMA("global_load_lds_dwordx4");
+  MLA_LDS_DMA("global_load_lds_dwordx4 %2, off");
 }
-__device__ __forceinline__ void dma4_to_lds(const void* g, uint32_t lds_off) { MLA_LDS_DMA("global_load_lds_dword"); }
+// The same with the non-temporal hint (nt), for the cache rows, which are read
+// once.  Measured: with the default policy a decode that follows a large write
+// (the timing protocols' cache flush, or any producer of that size) runs 15-35 %
+// longer than after another decode, as if its reads paid for writing back what
+// the write left in the caches; with nt it runs as fast as after a decode.
+// Scale rows (7 tokens per 128-B line) and slot indices keep the default
+// policy and the line reuse it gives.
+__device__ __forceinline__ void dma16_to_lds_nt(const void* g, uint32_t lds_off) {
+  MLA_LDS_DMA("global_load_lds_dwordx4 %2, off nt");
+}
+__device__ __forceinline__ void dma4_to_lds(const void* g, uint32_t lds_off) { MLA_LDS_DMA("global_load_lds_dword %2, off"); }
 // two bytes per lane (2-byte aligned source): lane l's bytes land,
 // zero-extended, in the dword at M0 + 4 l
-__device__ __forceinline__ void dma2_to_lds(const void* g, uint32_t lds_off) { MLA_LDS_DMA("global_load_lds_ushort"); }
+__device__ __forceinline__ void dma2_to_lds(const void* g, uint32_t lds_off) { MLA_LDS_DMA("global_load_lds_ushort %2, off"); }
 // one byte per lane: lane l's byte lands, zero-extended, in the dword at M0 + 4 l
-__device__ __forceinline__ void dma1_to_lds(const void* g, uint32_t lds_off) { MLA_LDS_DMA("global_load_lds_ubyte"); }
+__device__ __forceinline__ void dma1_to_lds(const void* g, uint32_t lds_off) { MLA_LDS_DMA("global_load_lds_ubyte %2, off"); }
 #undef MLA_LDS_DMA
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
