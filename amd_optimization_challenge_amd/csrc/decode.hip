@@ -180,7 +180,7 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
       const WavePlan P = plan_wave(p.kv_indptr, p.batch, p.plan_qlen, p.plan_target, p.plan_min_chunk,
                                    p.plan_max_splits);
       if (blockIdx.x == 0) plan_wave_write_rows(P, p.batch, p.max_items, const_cast<int32_t*>(plan));
-      const int4 mine = plan_wave_item(P, (int)blockIdx.x);
+      const int4 mine = plan_wave_item_uniform(P, (int)blockIdx.x);
       if ((threadIdx.x & 63) == 0) s_item = mine;
     }
     __syncthreads();
@@ -423,39 +423,37 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
       lds_barrier();  // every wave holds its fragments (and its row exponent) before the stage is refilled
     } else if constexpr (QM == 4) {
       // per head row: the per-tensor rule with the row as the tensor (|q| max,
-      // bf16 scale amax / 448), every row quantized at its own scale
+      // bf16 scale amax / 448), every row quantized at its own scale.  Lane
+      // group (w, lane / 16) holds head row 4w + lane / 16 and its lanes the
+      // 16-B chunks lane % 16 + 16k of it (72 a row): the row max is a 16-lane
+      // reduction and each lane forms its row's scale once.
       uint8_t* qst = smem + (C::S - 1) * C::STAGE;
-      uint32_t* rmax = reinterpret_cast<uint32_t*>(smem + C::OFF_X);  // [16] row maxima (bf16 bits)
-      if (tid < 16) rmax[tid] = 0;
-      uint4 xv[QNJ];
+      float* rsc = reinterpret_cast<float*>(smem + C::OFF_X);  // [16] row scales
+      constexpr int CPR = kQKDim / 8, NK = (CPR + 15) / 16;
+      const int qrow = 4 * w + (lane >> 4), c0 = lane & 15;
+      uint4 xv[NK];
+      uint32_t m = 0;
 #pragma unroll
-      for (int j = 0; j < QNJ; ++j) {
-        const int i = tid + 256 * j;
-        if (i < QNV) xv[j] = *reinterpret_cast<const uint4*>(qst + 16 * i);
+      for (int k = 0; k < NK; ++k) {
+        const int cc = c0 + 16 * k;
+        xv[k] = cc < CPR ? *reinterpret_cast<const uint4*>(qst + 16 * (qrow * CPR + cc)) : make_uint4(0, 0, 0, 0);
+        const uint32_t wv[4] = {xv[k].x, xv[k].y, xv[k].z, xv[k].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) m = max(m, max(wv[e] & 0x7FFFu, (wv[e] >> 16) & 0x7FFFu));
       }
-      lds_barrier();  // rmax zeroed
 #pragma unroll
-      for (int j = 0; j < QNJ; ++j) {
-        const int i = tid + 256 * j;
-        if (i < QNV) {
-          const uint32_t wv[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
-          uint32_t m = 0;
+      for (int msk = 1; msk < 16; msk <<= 1) m = max(m, (uint32_t)__shfl_xor((int)m, msk, 64));
+      const Fp8Quant qq = make_fp8_quant(fp8_scale_from_amax(m));
+      if (c0 == 0) rsc[qrow] = qq.s;
+      lds_barrier();  // every bf16 chunk read before the fp8 rows overwrite them
 #pragma unroll
-          for (int k = 0; k < 4; ++k) m = max(m, max(wv[k] & 0x7FFFu, (wv[k] >> 16) & 0x7FFFu));
-          atomicMax(&rmax[i / (kQKDim / 8)], m);
-        }
-      }
-      lds_barrier();  // row maxima complete; every bf16 chunk read before the fp8 rows overwrite them
-#pragma unroll
-      for (int j = 0; j < QNJ; ++j) {
-        const int i = tid + 256 * j;
-        if (i < QNV)
-          *reinterpret_cast<uint2*>(qst + 8 * i) =
-              quant8_fp8(xv[j], make_fp8_quant(fp8_scale_from_amax(rmax[i / (kQKDim / 8)])));
+      for (int k = 0; k < NK; ++k) {
+        const int cc = c0 + 16 * k;
+        if (cc < CPR) *reinterpret_cast<uint2*>(qst + 8 * (qrow * CPR + cc)) = quant8_fp8(xv[k], qq);
       }
       lds_barrier();
       load_q(qst + l16 * kQKDim);
-      c = fp8_scale_from_amax(rmax[l16]) * (KF == 0 ? kvs : 1.0f) * p.sm_scale * kLog2e;
+      c = rsc[l16] * (KF == 0 ? kvs : 1.0f) * p.sm_scale * kLog2e;
       lds_barrier();  // every wave holds its fragments and its row's scale before the stage is refilled
     } else if constexpr (QB) {
       uint8_t* qst = smem + (C::S - 1) * C::STAGE;

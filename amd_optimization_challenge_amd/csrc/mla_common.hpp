@@ -208,11 +208,28 @@ __device__ __forceinline__ uint32_t pack4_fp8_over(uint32_t old, float a, float 
 // eight bf16 (one uint4) -> eight e4m3fn codes of the per-tensor quantizer; the
 // hardware convert rounds to nearest even like the reference cast, and after
 // the clamp to +-448 no input can overflow it
+// (quant_y's rule, with the near-tie test folded over the eight elements so
+// that the division path is one branch per eight, taken only when some lane
+// needs it)
 __device__ __forceinline__ uint2 quant8_fp8(uint4 v, Fp8Quant q) {
-  return make_uint2(pack4_fp8(quant_y(v.x & 0xFFFFu, q), quant_y(v.x >> 16, q), quant_y(v.y & 0xFFFFu, q),
-                              quant_y(v.y >> 16, q)),
-                    pack4_fp8(quant_y(v.z & 0xFFFFu, q), quant_y(v.z >> 16, q), quant_y(v.w & 0xFFFFu, q),
-                              quant_y(v.w >> 16, q)));
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+  auto x = [&](int e) { return bf16_bits_to_f32(e & 1 ? w[e >> 1] >> 16 : w[e >> 1] & 0xFFFFu); };
+  float d[8];
+  bool slow = q.r == 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    d[e] = x(e) * q.r;
+    slow |= (__float_as_uint(d[e]) & 0xFFFFu) - 0x7FFDu <= 6u;
+  }
+  if (slow) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if (q.r == 0.0f || (__float_as_uint(d[e]) & 0xFFFFu) - 0x7FFDu <= 6u) d[e] = x(e) / q.s;
+  }
+  float y[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) y[e] = fminf(fmaxf(bf16_bits_to_f32(f32_to_bf16_bits(d[e])), -448.0f), 448.0f);
+  return make_uint2(pack4_fp8(y[0], y[1], y[2], y[3]), pack4_fp8(y[4], y[5], y[6], y[7]));
 }
 
 // ---- LDS DMA (global_load_lds) and explicit waits --------------------------

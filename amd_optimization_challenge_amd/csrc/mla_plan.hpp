@@ -53,10 +53,15 @@ __device__ __forceinline__ WavePlan plan_wave(const int32_t* __restrict__ kv_ind
   P.hi64 = (unsigned)wave_sum(L >> 6);
   P.lo64 = (unsigned)wave_sum(L & 63);
   const int lmax = wave_max(L);
+  const int L64 = (L + 63) >> 6;  // ceil(L / (64 m)) = ceil(L64 / m)
+  const unsigned s64 = (unsigned)wave_sum(L64);
   int lo = max(min_chunk / 64, (int)tiles_per_item(P.hi64, P.lo64, target_items));
   if (max_splits > 0) lo = max(lo, ((lmax + 63) / 64 + max_splits - 1) / max_splits);
-  int hi = max(lo, (lmax + 63) / 64);
-  const int L64 = (L + 63) >> 6;  // ceil(L / (64 m)) = ceil(L64 / m)
+  // m = ceil(s64 / (target - batch)) already fits: the count at m is at most
+  // sum(L64 / m + 1) <= s64 / m + batch <= target
+  int hi = (lmax + 63) / 64;
+  if (target_items > batch) hi = min(hi, (int)((s64 + (unsigned)(target_items - batch) - 1u) / (unsigned)(target_items - batch)));
+  hi = max(lo, hi);
   while (lo < hi) {
     const int mid = (lo + hi) >> 1;
     const int cnt = wave_sum(act ? (L64 > 0 ? (L64 + mid - 1) / mid : 1) : 0);
@@ -67,15 +72,29 @@ __device__ __forceinline__ WavePlan plan_wave(const int32_t* __restrict__ kv_ind
   P.nb = act ? (L > 0 ? (L64 + lo - 1) / lo : 1) : 0;
   const int piece = act ? (L > 0 ? (L + P.nb - 1) / P.nb : 0) : -1;
   // rank by piece length, longest first (ties by index); inactive lanes (piece
-  // -1) never count and rank last.  All 64 lanes are read with constant lane
+  // -1) never count and rank last.  Equal pieces on every row (a common
+  // batch) leave the rows in index order.  Otherwise key = (piece + 1) 64 +
+  // 63 - lane orders both at once (unique, the inactive lanes' keys below the
+  // rest) while it fits 31 bits, and the rank is the number of larger keys:
+  // one readlane, compare and add per lane, all 64 read with constant lane
   // indices, so the loop unrolls into independent readlanes.
-  int rank = 0;
+  int rank = lane;
+  const int pmax = wave_max(piece), pmin = -wave_max(act ? -piece : -0x7FFFFFFF);
+  if (pmin != pmax) {
+    rank = 0;
+    if (pmax < (1 << 24)) {
+      const int key = (piece + 1) * 64 + 63 - lane;
 #pragma unroll
-  for (int b2 = 0; b2 < 64; ++b2) {
-    const int p2 = __builtin_amdgcn_readlane(piece, b2);
-    rank += (p2 > piece) || (p2 == piece && b2 < lane);
+      for (int b2 = 0; b2 < 64; ++b2) rank += __builtin_amdgcn_readlane(key, b2) > key;
+    } else {
+#pragma unroll
+      for (int b2 = 0; b2 < 64; ++b2) {
+        const int p2 = __builtin_amdgcn_readlane(piece, b2);
+        rank += (p2 > piece) || (p2 == piece && b2 < lane);
+      }
+    }
+    if (!act) rank = lane;
   }
-  if (!act) rank = lane;
   // item counts in rank order -> inclusive scan -> each row's first item
   P.nb_r = __builtin_amdgcn_ds_permute(rank << 2, P.nb);
   P.x = wave_incl_sum(P.nb_r);
@@ -105,6 +124,25 @@ __device__ __forceinline__ int4 plan_wave_item(const WavePlan& P, int i) {
   const int nbb = __builtin_amdgcn_ds_bpermute(c << 2, P.nb_r);
   const int fb = __builtin_amdgcn_ds_bpermute(c << 2, P.x - P.nb_r);
   if (i >= P.n_items || nbb <= 0) return make_int4(-1, 0, 0, -1);
+  const unsigned j = (unsigned)(i - fb), n = (unsigned)nbb;
+  const unsigned q = (unsigned)lb / n, r = (unsigned)lb - q * n;
+  const int t0 = sb + (int)(j * q + (j * r) / n);
+  const int t1 = sb + (int)((j + 1) * q + ((j + 1) * r) / n);
+  return make_int4(bi, t0, t1, nbb > 1 ? i : -1);
+}
+
+// The same for a wave-uniform i (a work-group's own item): x is non-decreasing
+// in rank order, so the rank #{r : x_r <= i} is one ballot's population, and
+// the rank's fields are read from its lane.
+__device__ __forceinline__ int4 plan_wave_item_uniform(const WavePlan& P, int i) {
+  if (i >= P.n_items) return make_int4(-1, 0, 0, -1);
+  const int c = (int)__builtin_popcountll(__builtin_amdgcn_ballot_w64(P.x <= i));  // < 64: i < x_63
+  const int bi = __builtin_amdgcn_readlane(P.seq_r, c);
+  const int sb = __builtin_amdgcn_readlane(P.s0_r, c);
+  const int lb = __builtin_amdgcn_readlane(P.len_r, c);
+  const int nbb = __builtin_amdgcn_readlane(P.nb_r, c);
+  const int fb = __builtin_amdgcn_readlane(P.x, c) - nbb;
+  if (nbb <= 0) return make_int4(-1, 0, 0, -1);
   const unsigned j = (unsigned)(i - fb), n = (unsigned)nbb;
   const unsigned q = (unsigned)lb / n, r = (unsigned)lb - q * n;
   const int t0 = sb + (int)(j * q + (j * r) / n);
