@@ -540,9 +540,10 @@ int mla_decode_fwd_rowq(const void* q_bf16, const void* k_cache, int64_t k_row_s
   p.q_per_row = 1;
   int grid = L.max_items;
   hipError_t e;
-  if (batch <= 64) {
-    // the decode plans its own work: one launch fewer; at most t.items items
-    // for <= 64 rows (the planner's chunk search keeps the count within the target)
+  if (batch <= 256) {
+    // the decode plans its own work (one wave up to 64 rows, the block up to
+    // 256): one launch fewer; at most max(t.items, batch) items (the chunk
+    // search keeps the count within the target, or one piece per row)
     p.plan_here = 1;
     p.plan_qlen = q_seq_len;
     p.plan_target = t.items;

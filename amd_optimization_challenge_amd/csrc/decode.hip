@@ -160,7 +160,8 @@ constexpr int kVScaleSpan = 31;  // fp4 V: P' = P 2^(e - E_ref) <= 2^(96 + 31) s
 // (the lo one with B scale 2^-4), about 8 significant bits of Q as bf16 has.
 // 3: bf16, used as it is (a16w16, bf16 K).  4: bf16, quantized here per
 // head row (the per-tensor rule with the row as the tensor; fp8 or fp4 K), so
-// no tensor-wide amax pass has to run first.
+// no tensor-wide amax pass has to run first.  5: as 4, the work-group's item
+// planned here by the block (65 to 256 query rows).
 template <int KF, int VF, bool IDX, int QM>
 __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_kernel(const DecodeParams p) {
   using C = H16<KF, VF>;
@@ -172,16 +173,45 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
 
   const int32_t* plan = p.plan;
   int4 it;
-  if (QM == 4 && p.plan_here) {  // only the per-row Q route plans here
-    // wave 0 plans the (<= 64) rows in registers and takes this work-group's
-    // item; work-group 0 also writes what the combine reads of the plan
+  if (QM == 5 || (QM == 4 && p.plan_here)) {  // only the per-row Q route plans here
+    // QM 4, up to 64 rows: wave 0 plans in registers and takes this
+    // work-group's item; QM 5, up to 256: the block plans (its scratch on the
+    // ring, which nothing has written yet) and the thread of the item's row
+    // takes it (a variant of its own, so that the small batches' kernel does
+    // not carry the block planner's code).  Work-group 0 also writes what the
+    // combine reads of the plan.
     __shared__ int4 s_item;
-    if ((threadIdx.x >> 6) == 0) {
-      const WavePlan P = plan_wave(p.kv_indptr, p.batch, p.plan_qlen, p.plan_target, p.plan_min_chunk,
-                                   p.plan_max_splits);
-      if (blockIdx.x == 0) plan_wave_write_rows(P, p.batch, p.max_items, const_cast<int32_t*>(plan));
-      const int4 mine = plan_wave_item_uniform(P, (int)blockIdx.x);
-      if ((threadIdx.x & 63) == 0) s_item = mine;
+    if constexpr (QM == 4) {
+      if ((threadIdx.x >> 6) == 0) {
+        const WavePlan P = plan_wave(p.kv_indptr, p.batch, p.plan_qlen, p.plan_target, p.plan_min_chunk,
+                                     p.plan_max_splits);
+        if (blockIdx.x == 0) plan_wave_write_rows(P, p.batch, p.max_items, const_cast<int32_t*>(plan));
+        const int4 mine = plan_wave_item_uniform(P, (int)blockIdx.x);
+        if ((threadIdx.x & 63) == 0) s_item = mine;
+      }
+    } else {
+      const BlockPlan P = plan_block(p.kv_indptr, p.batch, p.plan_qlen, p.plan_target, p.plan_min_chunk,
+                                     p.plan_max_splits, reinterpret_cast<uint64_t*>(smem),
+                                     reinterpret_cast<int*>(smem + 2048), reinterpret_cast<int*>(smem + 3072));
+      const int tid = threadIdx.x, i = blockIdx.x;
+      if (blockIdx.x == 0) {
+        int32_t* pl = const_cast<int32_t*>(plan);
+        if (tid < p.batch) reinterpret_cast<int2*>(pl + kPlanHeader + 4 * p.max_items)[tid] = make_int2(P.first, P.nb);
+        if (tid == 0) {
+          pl[0] = P.n_items;
+          pl[1] = P.chunk;
+          pl[2] = (int)(64u * P.hi64 + P.lo64);
+          pl[3] = p.batch;
+          pl[4] = p.max_items;
+        }
+      }
+      if (tid == 0 && i >= P.n_items) s_item = make_int4(-1, 0, 0, -1);
+      if (tid < p.batch && P.first <= i && i < P.first + P.nb) {  // piece j of this row, as the planner emits it
+        const unsigned j = (unsigned)(i - P.first), n = (unsigned)P.nb;
+        const unsigned q = (unsigned)P.L / n, r = (unsigned)P.L - q * n;
+        s_item = make_int4(tid, P.s0 + (int)(j * q + (j * r) / n), P.s0 + (int)((j + 1) * q + ((j + 1) * r) / n),
+                           P.nb > 1 ? i : -1);
+      }
     }
     __syncthreads();
     it = s_item;
@@ -421,7 +451,7 @@ __global__ __launch_bounds__(256, (H16<KF, VF>::BLOCKS_PER_CU)) void decode_h16_
       for (int ks = 0; ks < 5; ++ks) asm volatile("" : "+v"(qlo[ks]));
       c = __builtin_amdgcn_ldexpf(1.0f, (int)rmax[16 + l16]) * kvs * p.sm_scale * kLog2e;
       lds_barrier();  // every wave holds its fragments (and its row exponent) before the stage is refilled
-    } else if constexpr (QM == 4) {
+    } else if constexpr (QM == 4 || QM == 5) {
       // per head row: the per-tensor rule with the row as the tensor (|q| max,
       // bf16 scale amax / 448), every row quantized at its own scale.  Lane
       // group (w, lane / 16) holds head row 4w + lane / 16 and its lanes the
@@ -891,9 +921,16 @@ static hipError_t launch_decode_t(const DecodeParams& p, int kv_mode, int grid, 
       return hipGetLastError();
     }
     if (QB && p.q_per_row) {  // bf16 Q quantized per head row here (fp8 or mxfp4 cache)
+      const bool blk = p.plan_here && p.batch > 64;  // the block plans in the kernel
       switch (kv_mode) {
-        case 0: hipLaunchKernelGGL((decode_h16_kernel<0, 0, IDX, 4>), dim3(grid), dim3(256), 0, stream, p); break;
-        case 1: hipLaunchKernelGGL((decode_h16_kernel<1, 2, IDX, 4>), dim3(grid), dim3(256), 0, stream, p); break;
+        case 0:
+          if (blk) hipLaunchKernelGGL((decode_h16_kernel<0, 0, IDX, 5>), dim3(grid), dim3(256), 0, stream, p);
+          else hipLaunchKernelGGL((decode_h16_kernel<0, 0, IDX, 4>), dim3(grid), dim3(256), 0, stream, p);
+          break;
+        case 1:
+          if (blk) hipLaunchKernelGGL((decode_h16_kernel<1, 2, IDX, 5>), dim3(grid), dim3(256), 0, stream, p);
+          else hipLaunchKernelGGL((decode_h16_kernel<1, 2, IDX, 4>), dim3(grid), dim3(256), 0, stream, p);
+          break;
         default: return hipErrorInvalidValue;
       }
       return hipGetLastError();

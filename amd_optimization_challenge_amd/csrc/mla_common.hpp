@@ -49,7 +49,7 @@ struct DecodeParams {
   int num_heads;
   int max_items;
   // 16 heads: q_per_row = bf16 Q quantized per head row in the kernel (no
-  // tensor-wide scale); plan_here = the kernel plans its own work (batch <= 64
+  // tensor-wide scale); plan_here = the kernel plans its own work (batch <= 256
   // query rows, plan_qlen per sequence) with the planner's target, chunk floor
   // and split cap, and its work-group 0 writes the rows' piece counts and the
   // header the combine reads (plan then points at writable workspace)

@@ -1,8 +1,8 @@
-// The split planner's one-wave form (up to 64 query rows), shared by the
-// planner kernel (which writes every item) and the 16-head decode kernel
-// when it plans its own work (it needs one item; its work-group 0 writes the
-// rows' piece counts and the header the combine reads).  The plan itself is
-// described in quant.hip.
+// The split planner's one-wave form (up to 64 query rows) and block form (up
+// to 256), shared by the planner kernel (which writes every item) and the
+// 16-head decode kernel when it plans its own work (it needs one item; its
+// work-group 0 writes the rows' piece counts and the header the combine
+// reads).  The plan itself is described in quant.hip.
 #pragma once
 
 #include "mla_common.hpp"
@@ -162,6 +162,106 @@ __device__ __forceinline__ void plan_wave_write_rows(const WavePlan& P, int batc
     plan[3] = batch;
     plan[4] = max_items;
   }
+}
+
+// sum / max of one non-negative int per thread over the 256-thread block
+// (`red` holds 4 ints; every thread gets the result)
+__device__ __forceinline__ int block_sum(int v, int* red) {
+  const int t = wave_sum(v);
+  __syncthreads();  // red free
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = t;
+  __syncthreads();
+  return red[0] + red[1] + red[2] + red[3];
+}
+__device__ __forceinline__ int block_max(int v, int* red) {
+  const int t = wave_max(v);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = t;
+  __syncthreads();
+  return max(max(red[0], red[1]), max(red[2], red[3]));
+}
+
+// exclusive scan of one int per thread over the 256-thread block; *total =
+// the block sum (same in every thread)
+__device__ __forceinline__ int block_exscan(int v, int* red, int* total) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int x = wave_incl_sum(v);
+  __syncthreads();  // red free
+  if (lane == 63) red[w] = x;
+  __syncthreads();
+  int base = 0;
+  for (int i = 0; i < w; ++i) base += red[i];
+  *total = red[0] + red[1] + red[2] + red[3];
+  return base + x - v;
+}
+
+// Up to 256 rows, one per thread of a 256-thread block (every thread must
+// call it): the block form of the plan, which the planner kernel uses above
+// 64 rows and the 16-head decode for up to 256.  Thread b < batch gets row
+// b's length, piece count, first key and first item; every thread gets the
+// chunk, the item count and the length sums.  Scratch: 256 keys, 256 counts
+// and 4 ints of LDS; it ends with a barrier after its last scratch read.
+struct BlockPlan {
+  int chunk, n_items;
+  unsigned hi64, lo64;
+  int L, nb, s0, first;
+};
+__device__ __forceinline__ BlockPlan plan_block(const int32_t* __restrict__ kv_indptr, int batch, int qlen,
+                                                int target_items, int min_chunk, int max_splits,
+                                                uint64_t* s_key, int* s_cnt, int* s_red) {
+  const int tid = threadIdx.x;
+  const bool act = tid < batch;
+  BlockPlan P;
+  P.L = act ? row_len(kv_indptr, tid, qlen) : 0;
+  P.s0 = act ? row_start(kv_indptr, tid, qlen) : 0;
+  P.hi64 = (unsigned)block_sum(P.L >> 6, s_red);
+  P.lo64 = (unsigned)block_sum(P.L & 63, s_red);
+  const int lmax = block_max(P.L, s_red);
+  int chunk = 64 * max(min_chunk / 64, (int)tiles_per_item(P.hi64, P.lo64, target_items));
+  if (max_splits > 0) chunk = max(chunk, 64 * (((lmax + 63) / 64 + max_splits - 1) / max_splits));
+  // binary search on chunk / 64 in [c0 / 64, ceil(lmax / 64)]
+  const int L64 = (P.L + 63) >> 6;
+  int lo = chunk / 64, hi = max(lo, (lmax + 63) / 64);
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    const int cnt = block_sum(act ? (L64 > 0 ? (L64 + mid - 1) / mid : 1) : 0, s_red);
+    if (cnt <= target_items) hi = mid;
+    else lo = mid + 1;
+  }
+  P.chunk = lo * 64;
+  P.nb = act ? (P.L > 0 ? (P.L + P.chunk - 1) / P.chunk : 1) : 0;
+  // rank rows by piece length, longest first (ties by index); equal pieces on
+  // every row leave them in index order.  Otherwise key = piece << 32 |
+  // (2^32 - 1 - b): a larger key ranks earlier, and "no row" is key 0, below
+  // every real one; two keys per 16-byte LDS read, one compare each.
+  const int piece = act ? (P.L > 0 ? (P.L + P.nb - 1) / P.nb : 0) : -1;
+  const int pmax = block_max(act ? piece : 0, s_red), npmin = block_max(act ? -piece : -0x7FFFFFFF, s_red);
+  int rank = tid;
+  if (pmax != -npmin) {
+    const uint64_t key = piece < 0 ? 0ull : ((uint64_t)(uint32_t)piece << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)tid);
+    s_key[tid] = key;
+    __syncthreads();
+    rank = 0;
+    if (act) {
+      const ulonglong2* kv = reinterpret_cast<const ulonglong2*>(s_key);
+#pragma unroll 8
+      for (int b2 = 0; b2 < (batch + 1) / 2; ++b2) {
+        const ulonglong2 q = kv[b2];
+        rank += (q.x > key) + (q.y > key);
+      }
+    }
+  }
+  if (act) s_cnt[rank] = P.nb;
+  __syncthreads();
+  int total = 0;
+  const int ex = block_exscan(tid < batch ? s_cnt[tid] : 0, s_red, &total);
+  __syncthreads();
+  if (tid < batch) s_cnt[tid] = ex;
+  __syncthreads();
+  P.first = act ? s_cnt[rank] : 0;
+  P.n_items = total;
+  __syncthreads();  // every scratch read done
+  return P;
 }
 
 }  // namespace mla

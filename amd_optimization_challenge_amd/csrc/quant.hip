@@ -279,37 +279,6 @@ __global__ __launch_bounds__(256) void append_kv_kernel(
 // ---------------------------------------------------------------------------
 constexpr int kPlanSortMax = 256;
 
-// sum / max of one non-negative int per thread over the 256-thread block
-// (`red` holds 4 ints; every thread gets the result)
-__device__ int block_sum(int v, int* red) {
-  const int t = wave_sum(v);
-  __syncthreads();  // red free
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = t;
-  __syncthreads();
-  return red[0] + red[1] + red[2] + red[3];
-}
-__device__ int block_max(int v, int* red) {
-  const int t = wave_max(v);
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = t;
-  __syncthreads();
-  return max(max(red[0], red[1]), max(red[2], red[3]));
-}
-
-// exclusive scan of one int per thread over the 256-thread block; *total =
-// the block sum (same in every thread)
-__device__ int block_exscan(int v, int* red, int* total) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int x = wave_incl_sum(v);
-  __syncthreads();  // red free
-  if (lane == 63) red[w] = x;
-  __syncthreads();
-  int base = 0;
-  for (int i = 0; i < w; ++i) base += red[i];
-  *total = red[0] + red[1] + red[2] + red[3];
-  return base + x - v;
-}
-
 // the nb near-equal pieces of [s0, s0 + L): piece i = [s0 + floor(iL/nb),
 // s0 + floor((i+1)L/nb)), computed with one division and a running remainder
 __device__ __forceinline__ void emit_pieces(int4* __restrict__ items, int b, int s0, int L, int nb, int first) {
@@ -355,85 +324,51 @@ __device__ __forceinline__ void build_plan(const int32_t* __restrict__ kv_indptr
   __shared__ __attribute__((aligned(16))) uint64_t s_key[kPlanSortMax];
   __shared__ int s_cnt[kPlanSortMax];    // item counts in layout order, then their exclusive scan
   const int tid = threadIdx.x;
+  int4* items = reinterpret_cast<int4*>(plan + kPlanHeader);
+  int2* binfo = reinterpret_cast<int2*>(plan + kPlanHeader + 4 * max_items);
+  if (batch <= kPlanSortMax) {
+    const BlockPlan P = plan_block(kv_indptr, batch, qlen, target_items, min_chunk, max_splits, s_key, s_cnt, s_red);
+    if (tid < batch) {
+      binfo[tid] = make_int2(P.first, P.nb);
+      emit_pieces(items, tid, P.s0, P.L, P.nb, P.first);
+    }
+    if (tid == 0) {
+      plan[0] = P.n_items;
+      plan[1] = P.chunk;
+      plan[2] = (int)(64u * P.hi64 + P.lo64);
+      plan[3] = batch;
+      plan[4] = max_items;
+    }
+    return;
+  }
   int t_hi = 0, t_lo = 0, t_max = 0;
-  int own_s0 = 0;  // batch <= 256: this thread's row start (and t_max its length)
   for (int b = tid; b < batch; b += 256) {
     const int L = row_len(kv_indptr, b, qlen);
     t_hi += L >> 6;
     t_lo += L & 63;
     t_max = max(t_max, L);
-    own_s0 = row_start(kv_indptr, b, qlen);
   }
   const unsigned hi64 = (unsigned)block_sum(t_hi, s_red), lo64 = (unsigned)block_sum(t_lo, s_red);
   const int lmax = block_max(t_max, s_red);
   int chunk = 64 * max(min_chunk / 64, (int)tiles_per_item(hi64, lo64, target_items));
   if (max_splits > 0) chunk = max(chunk, 64 * (((lmax + 63) / 64 + max_splits - 1) / max_splits));
-  if (batch <= kPlanSortMax) {
-    // one sequence per thread: binary search on chunk / 64 in [c0 / 64, ceil(lmax / 64)]
-    const int L64 = (t_max + 63) >> 6;  // batch <= 256: t_max is this thread's own L
-    int lo = chunk / 64, hi = max(lo, (lmax + 63) / 64);
-    while (lo < hi) {
-      const int mid = (lo + hi) >> 1;
-      const int cnt = block_sum(tid < batch ? (L64 > 0 ? (L64 + mid - 1) / mid : 1) : 0, s_red);
-      if (cnt <= target_items) hi = mid;
-      else lo = mid + 1;
-    }
-    chunk = lo * 64;
-  }
-  auto len_of = [&](int b) { return row_len(kv_indptr, b, qlen); };
+  // more sequences than one block sorts: layout order, one 256-row pass at a time
   auto nb_of = [&](int L) { return L > 0 ? (L + chunk - 1) / chunk : 1; };
-  int4* items = reinterpret_cast<int4*>(plan + kPlanHeader);
-  int2* binfo = reinterpret_cast<int2*>(plan + kPlanHeader + 4 * max_items);
-  auto emit = [&](int b, int L, int nb, int first, int s0) {
-    binfo[b] = make_int2(first, nb);
-    emit_pieces(items, b, s0, L, nb, first);
-  };
   int carry = 0;
-  if (batch <= kPlanSortMax) {
-    // rank sequences by piece length, longest first (ties by index)
-    const int b = tid;
-    int L = 0, nb = 0, piece = -1;  // -1: no sequence (never counts in a rank)
+  for (int base = 0; base < batch; base += 256) {
+    const int b = base + tid;
+    int L = 0, nb = 0;
     if (b < batch) {
-      L = t_max;  // this thread's own row, read in the first pass
+      L = row_len(kv_indptr, b, qlen);
       nb = nb_of(L);
-      piece = (L + nb - 1) / nb;
     }
-    // key = piece << 32 | (2^32 - 1 - b): a larger key ranks earlier, and
-    // "no sequence" (piece -1) is key 0, below every real one
-    const uint64_t key = piece < 0 ? 0ull : ((uint64_t)(uint32_t)piece << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)b);
-    if (b < kPlanSortMax) s_key[b] = key;
-    __syncthreads();
-    int rank = 0;
+    int tot = 0;
+    const int ex = block_exscan(nb, s_red, &tot);
     if (b < batch) {
-      // two keys per 16-byte LDS read, several reads in flight; one compare each
-      const ulonglong2* kv = reinterpret_cast<const ulonglong2*>(s_key);
-#pragma unroll 8
-      for (int b2 = 0; b2 < (batch + 1) / 2; ++b2) {
-        const ulonglong2 q = kv[b2];
-        rank += (q.x > key) + (q.y > key);
-      }
-      s_cnt[rank] = nb;
+      binfo[b] = make_int2(carry + ex, nb);
+      emit_pieces(items, b, row_start(kv_indptr, b, qlen), L, nb, carry + ex);
     }
-    __syncthreads();
-    const int v = tid < batch ? s_cnt[tid] : 0;
-    const int ex = block_exscan(v, s_red, &carry);
-    __syncthreads();
-    if (tid < batch) s_cnt[tid] = ex;
-    __syncthreads();
-    if (b < batch) emit(b, L, nb, s_cnt[rank], own_s0);
-  } else {
-    for (int base = 0; base < batch; base += 256) {
-      const int b = base + tid;
-      int L = 0, nb = 0;
-      if (b < batch) {
-        L = len_of(b);
-        nb = nb_of(L);
-      }
-      int tot = 0;
-      const int ex = block_exscan(nb, s_red, &tot);
-      if (b < batch) emit(b, L, nb, carry + ex, row_start(kv_indptr, b, qlen));
-      carry += tot;
-    }
+    carry += tot;
   }
   if (tid == 0) {
     plan[0] = carry;

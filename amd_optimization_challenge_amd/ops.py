@@ -279,7 +279,7 @@ def decode_fwd(q, kv_data, kv_indptr, kv_indices, sm_scale, kv_mode="fp8", out=N
     q_dtype "bf16": the a16w8 route (``mla_decode_fwd_a16w8``; 16 heads, fp8
     cache): Q keeps its own precision, no per-tensor quantization.  q_dtype
     "fp8_row" (``mla_decode_fwd_rowq``; 16 heads, fp8 or mxfp4 cache): Q
-    quantized per head row inside the decode, which for up to 64 query rows
+    quantized per head row inside the decode, which for up to 256 query rows
     also plans its own work (two launches per call).
     """
     if int(page_size) != 1:

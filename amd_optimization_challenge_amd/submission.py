@@ -63,7 +63,7 @@ def custom_kernel(data: input_t) -> output_t:
     q_dtype = config.get("q_dtype", "fp8")
     if kv_mode == "auto":
         kv_mode = auto_kv_mode(num_heads, kv_data)
-        # 16 heads: Q quantized per head row in the decode, which for <= 64
+        # 16 heads: Q quantized per head row in the decode, which for <= 256
         # query rows also plans its own work (decode + combine: no amax pass)
         q_dtype = config.get("q_dtype", "fp8_row" if num_heads == 16 else "fp8")
     kv_indices = config.get("kv_indices")

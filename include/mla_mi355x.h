@@ -224,7 +224,7 @@ int mla_decode_fwd_a16w8(const void* q_bf16, const void* k_cache, int64_t k_row_
  * mla_decode_fwd with Q quantized per head row instead of per tensor: each
  * [576] row of bf16 Q gets the per-tensor rule of quantize_fp8
  * (TASK/reference.py:76-80) with the row as the tensor, inside the decode
- * kernel, so no tensor-wide amax pass runs first; for batch <= 64 query rows
+ * kernel, so no tensor-wide amax pass runs first; for batch <= 256 query rows
  * the decode kernel also plans its own work, so the call is two launches
  * (decode, combine).  16 heads, the fp8 or the mxfp4 cache.  It replaces the
  * reference's small-shape route, which quantizes Q per 32-element MXFP4 block

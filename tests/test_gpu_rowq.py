@@ -1,10 +1,11 @@
 """The per-row Q route (``mla_decode_fwd_rowq``): bf16 Q quantized per head
-row inside the 16-head decode, which for up to 64 query rows also plans its
+row inside the 16-head decode, which for up to 256 query rows also plans its
 own work (decode + combine, two launches).  Parity against the oracle's
 per-row path (atol = rtol = 2e-2 and rel-L2), indexed and contiguous, both
-caches, short / ragged / empty rows, past 64 rows (the planner kernel), causal
-rows with LSE; the plan the decode's work-group 0 leaves in the workspace
-equals the planner kernel's for the same target."""
+caches, short / ragged / empty rows, past 64 rows (the block plans in the
+kernel), past 256 (the planner kernel runs first), causal rows with LSE; the
+plan the decode's work-group 0 leaves in the workspace equals the planner
+kernel's for the same target."""
 import math
 
 import numpy as np
@@ -22,7 +23,9 @@ SM = 1 / math.sqrt(192)
 @pytest.mark.parametrize("contig", [False, True])
 @pytest.mark.parametrize("mode", ["fp8", "mxfp4"])
 @pytest.mark.parametrize("lens", [[1, 63, 64, 65], [3000, 10, 129, 700, 1], [0, 200, 7], [1024] * 32,
-                                  [(i * 37) % 700 + 1 for i in range(80)]])
+                                  [(i * 37) % 700 + 1 for i in range(80)], [96] * 256,
+                                  [0 if i % 11 == 0 else (i * 53) % 400 + 1 for i in range(200)],
+                                  [(i * 13) % 90 + 1 for i in range(300)]])
 def test_rowq_matches_oracle(cuda, mode, lens, contig):
     print(f"rowq mode={mode} B={len(lens)} contig={contig}", flush=True)
     q, kv, indptr, idx, qb, caches = host_case(lens, 16, mode, seed=len(lens) + 3, permute=not contig)
@@ -62,7 +65,9 @@ def test_rowq_causal_rows_and_lse(cuda, mode, qlen):
 
 
 @pytest.mark.parametrize("mode", ["fp8", "mxfp4"])
-@pytest.mark.parametrize("lens", [[3000, 10, 129, 700, 1], [(i * 7919) % 9000 + 1 for i in range(64)], [5] * 3])
+@pytest.mark.parametrize("lens", [[3000, 10, 129, 700, 1], [(i * 7919) % 9000 + 1 for i in range(64)], [5] * 3,
+                                  [(i * 7919) % 3000 + 1 for i in range(200)], [512] * 256,
+                                  [0 if i % 7 == 0 else (i * 31) % 1500 + 1 for i in range(130)]])
 def test_in_kernel_plan_equals_planner_kernel(cuda, mode, lens):
     """Indexed rows: the in-kernel plan targets what mla_plan targets, so the
     rows' (first item, piece count) and the header the decode's work-group 0
