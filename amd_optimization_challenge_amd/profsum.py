@@ -1,16 +1,17 @@
 """Summaries of rocprofv3 CSV output for this operator's profiles.
 
-    python -m amd_optimization_challenge_amd.profsum trace  <p_kernel_trace.csv> [--timed K]
+    python -m amd_optimization_challenge_amd.profsum trace  <p_kernel_trace.csv> [--timed K] [--replays R]
     python -m amd_optimization_challenge_amd.profsum pmc    <fetch counter_collection.csv> <write counter_collection.csv>
     python -m amd_optimization_challenge_amd.profsum sq     <counter_collection.csv> [--match NAME]
 
 trace: per-kernel calls / total / mean / min / max, then every run of at
-least K back-to-back launches of one decode kernel (name and grid): the mean
-kernel duration of its last K and their launch period (first start to last
-end over K, which is what one event pair around the run measures: the kernel
-plus the boundary to the next one); these are the bench's decode-only runs
-over rotating cache copies.  The other decode launches (inside whole calls)
-are averaged per kernel.
+least K back-to-back launches of one decode kernel (name and grid): split
+its last R K launches into R blocks of K (the bench's timed graph replays),
+the median over the blocks of their mean kernel duration and of their launch
+period (first start to last end over K, which is what one event pair around
+a replay measures: the kernel plus the boundary to the next one); these are
+the bench's decode-only runs over rotating cache copies.  The other decode
+launches (inside whole calls) are averaged per kernel.
 
 pmc: FETCH_SIZE and WRITE_SIZE (KiB per dispatch) of every run of decode
 launches separated only by the flush fill (a set-up kernel starts a new run),
@@ -29,6 +30,7 @@ from __future__ import annotations
 import argparse
 import collections
 import csv
+import statistics
 import sys
 
 DECODE = ("decode_h16_kernel", "decode_h128_kernel")
@@ -52,7 +54,7 @@ def read_trace(path):
     return out
 
 
-def trace_summary(path, timed):
+def trace_summary(path, timed, replays=1):
     ks = read_trace(path)
     agg = collections.OrderedDict()
     for k in ks:
@@ -63,8 +65,9 @@ def trace_summary(path, timed):
     for name, d in sorted(agg.items(), key=lambda kv: -sum(kv[1])):
         lines.append(f"| `{name}` | {len(d)} | {sum(d) / 1e3:.1f} | {sum(d) / len(d) / 1e3:.2f} | {min(d) / 1e3:.2f} | "
                      f"{max(d) / 1e3:.2f} | {100 * sum(d) / total:.2f} |")
-    lines += ["", f"Decode kernels: each run of at least {timed} back-to-back launches (decode only; the mean of "
-                  f"its last {timed}), then the launches inside whole calls per kernel.", "",
+    lines += ["", f"Decode kernels: each run of at least {timed} back-to-back launches (decode only; the median "
+                  f"over its last {replays} blocks of {timed} of their means), then the launches inside whole calls "
+                  f"per kernel.", "",
               "| # | kernel | grid (threads) | run length | kernel avg us | launch period us |", "|---|---|---|---|---|---|"]
     runs, incall, cur = [], collections.OrderedDict(), None
     for k in ks:
@@ -81,9 +84,13 @@ def trace_summary(path, timed):
     for key, r in runs:
         if len(r) >= timed:
             n += 1
-            t = r[-timed:]
-            dur = sum(k["end"] - k["start"] for k in t) / len(t)
-            period = (t[-1]["end"] - t[0]["start"]) / len(t)  # what one event pair around the run measures
+            nb = max(1, min(replays, len(r) // timed))
+            durs, periods = [], []
+            for j in range(nb):
+                t = r[len(r) - (nb - j) * timed:len(r) - (nb - j - 1) * timed]
+                durs.append(sum(k["end"] - k["start"] for k in t) / len(t))
+                periods.append((t[-1]["end"] - t[0]["start"]) / len(t))  # what one event pair around a replay measures
+            dur, period = statistics.median(durs), statistics.median(periods)
             lines.append(f"| {n} | `{key[0]}` | {key[1]} | {len(r)} | {dur / 1e3:.2f} | {period / 1e3:.2f} |")
         else:
             incall.setdefault(key, []).extend(k["end"] - k["start"] for k in r)
@@ -190,6 +197,7 @@ def main(argv=None) -> int:
     t = sub.add_parser("trace")
     t.add_argument("csv")
     t.add_argument("--timed", type=int, default=20)
+    t.add_argument("--replays", type=int, default=1, help="timed replays of K launches at the end of each run")
     p = sub.add_parser("pmc")
     p.add_argument("fetch_csv")
     p.add_argument("write_csv")
@@ -198,7 +206,7 @@ def main(argv=None) -> int:
     s.add_argument("--match", default=None, help="kernel-name substring (default: the decode kernels)")
     a = ap.parse_args(argv)
     if a.cmd == "trace":
-        print(trace_summary(a.csv, a.timed))
+        print(trace_summary(a.csv, a.timed, a.replays))
     elif a.cmd == "pmc":
         print(pmc_summary(a.fetch_csv, a.write_csv))
     else:

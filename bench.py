@@ -25,6 +25,7 @@ same rows, and the decode's fraction of it.
 from __future__ import annotations
 
 import argparse
+import statistics
 import json
 import math
 import os
@@ -229,13 +230,14 @@ def time_config(cid, steps, warmup, flush_buf, probe=True):
     copies = make_copies(kv_data, ncopy)
     args = (kv_indptr, cfg["kv_indices"], H, cfg["sm_scale"], mode, ws, out)
 
-    def time_decode(cs):
+    def time_decode(cs, replays=5):
         """us per launch: `steps` back-to-back launches captured in one HIP
-        graph, one event pair around a replay.  Eager launches from Python
-        arrive slower than a 10-us kernel runs (the GPU would wait on the
-        host), and an event pair per launch adds its own barrier, several us,
-        to every launch.  Each launch's share includes the boundary to the next
-        kernel.  The decode path records no memset and allocates nothing."""
+        graph, one event pair around each replay, the median over `replays`
+        timed replays.  Eager launches from Python arrive slower than a 10-us
+        kernel runs (the GPU would wait on the host), and an event pair per
+        launch adds its own barrier, several us, to every launch.  Each
+        launch's share includes the boundary to the next kernel.  The decode
+        path records no memset and allocates nothing."""
         for c in cs:  # warm-up: every copy once, eagerly
             ops.decode(qf8, qsc, c, *args)
         torch.cuda.synchronize()
@@ -245,13 +247,16 @@ def time_config(cid, steps, warmup, flush_buf, probe=True):
                 ops.decode(qf8, qsc, cs[i % len(cs)], *args)
         g.replay()  # warm-up replay
         torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        g.replay()
-        e1.record()
-        torch.cuda.synchronize()
+        us = []
+        for _ in range(replays):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            g.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            us.append(e0.elapsed_time(e1) * 1e3 / steps)
         del g
-        return e0.elapsed_time(e1) * 1e3 / steps
+        return statistics.median(us)
 
     dec_mean = time_decode(copies)
     ops.combine(B, H, ws, out)
