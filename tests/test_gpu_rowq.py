@@ -41,10 +41,12 @@ def test_rowq_matches_oracle(cuda, mode, lens, contig):
 
 
 @pytest.mark.parametrize("mode", ["fp8", "mxfp4"])
-@pytest.mark.parametrize("qlen", [2, 4])
-def test_rowq_causal_rows_and_lse(cuda, mode, qlen):
-    print(f"rowq causal mode={mode} qlen={qlen}", flush=True)
-    lens = [300, 7, 1, 64, 2000, 2]
+@pytest.mark.parametrize("qlen,lens", [(2, [300, 7, 1, 64, 2000, 2]), (4, [300, 7, 1, 64, 2000, 2]),
+                                       (4, [(i * 29) % 240 + 4 for i in range(40)])])
+def test_rowq_causal_rows_and_lse(cuda, mode, qlen, lens):
+    """Causal multi-token rows: 12 and 24 query rows (the wave plans) and 160
+    (the block plans)."""
+    print(f"rowq causal mode={mode} qlen={qlen} S={len(lens)}", flush=True)
     S = len(lens)
     g = torch.Generator().manual_seed(200 + qlen)
     q = torch.randn(S * qlen, 16, 576, generator=g).to(torch.bfloat16)
