@@ -592,8 +592,8 @@ def main(argv=None):
                     help="decode-only launches for counter collection (no JSON line)")
     args = ap.parse_args(argv)
     if args.gpus != 1:
-        print(json.dumps({"error": "this operator runs on one GPU; multi-GPU sharding is design-only "
-                                   "(DESIGN.md), run with --gpus 1"}))
+        print(json.dumps({"error": "this operator runs on one GPU (one process per GPU would shard the "
+                                   "batch's sequences; not built here): run with --gpus 1"}))
         return 2
     import torch
 
