@@ -62,6 +62,14 @@ __device__ __forceinline__ WavePlan plan_wave(const int32_t* __restrict__ kv_ind
   int hi = (lmax + 63) / 64;
   if (target_items > batch) hi = min(hi, (int)((s64 + (unsigned)(target_items - batch) - 1u) / (unsigned)(target_items - batch)));
   hi = max(lo, hi);
+  const int l64min = -wave_max(act ? -L64 : -0x7FFFFFFF);
+  if (l64min == (lmax + 63) / 64) {
+    // every row as long (a common batch): the count at m is batch ceil(L64 / m),
+    // so the smallest m in [lo, hi] within the target is ceil(L64 / k), k =
+    // target / batch pieces a row, clamped (hi when no m fits)
+    const int k = target_items / max(batch, 1);
+    lo = hi = k > 0 ? min(hi, max(lo, (l64min + k - 1) / k)) : hi;
+  }
   while (lo < hi) {
     const int mid = (lo + hi) >> 1;
     const int cnt = wave_sum(act ? (L64 > 0 ? (L64 + mid - 1) / mid : 1) : 0);
