@@ -208,27 +208,26 @@ __device__ __forceinline__ uint32_t pack4_fp8_over(uint32_t old, float a, float 
 // eight bf16 (one uint4) -> eight e4m3fn codes of the per-tensor quantizer; the
 // hardware convert rounds to nearest even like the reference cast, and after
 // the clamp to +-448 no input can overflow it
-// (quant_y's rule, with the near-tie test folded over the eight elements so
-// that the division path is one branch per eight, taken only when some lane
-// needs it)
+// Here x * r needs no near-tie test: x and s are both bf16, so x / s is a
+// ratio of 8-bit significands times a power of two, never a bf16 tie (a tie
+// would make an odd number equal to an even one) and at least 2^-17 of itself
+// away from one (|A - ms T| >= 1 for the integers A = mx 2^p, ms < 2^8 and the
+// tie's odd numerator T < 2^9), while x * r is within 2^-23 of x / s; and
+// results beyond 448 clamp to 448 either way.  The division remains for r = 0
+// (s infinite or NaN).
 __device__ __forceinline__ uint2 quant8_fp8(uint4 v, Fp8Quant q) {
   const uint32_t w[4] = {v.x, v.y, v.z, v.w};
   auto x = [&](int e) { return bf16_bits_to_f32(e & 1 ? w[e >> 1] >> 16 : w[e >> 1] & 0xFFFFu); };
-  float d[8];
-  bool slow = q.r == 0.0f;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    d[e] = x(e) * q.r;
-    slow |= (__float_as_uint(d[e]) & 0xFFFFu) - 0x7FFDu <= 6u;
-  }
-  if (slow) {
+  float y[8];
+  if (q.r != 0.0f) {
 #pragma unroll
     for (int e = 0; e < 8; ++e)
-      if (q.r == 0.0f || (__float_as_uint(d[e]) & 0xFFFFu) - 0x7FFDu <= 6u) d[e] = x(e) / q.s;
-  }
-  float y[8];
+      y[e] = fminf(fmaxf(bf16_bits_to_f32(f32_to_bf16_bits(x(e) * q.r)), -448.0f), 448.0f);
+  } else {
 #pragma unroll
-  for (int e = 0; e < 8; ++e) y[e] = fminf(fmaxf(bf16_bits_to_f32(f32_to_bf16_bits(d[e])), -448.0f), 448.0f);
+    for (int e = 0; e < 8; ++e)
+      y[e] = fminf(fmaxf(bf16_bits_to_f32(f32_to_bf16_bits(x(e) / q.s)), -448.0f), 448.0f);
+  }
   return make_uint2(pack4_fp8(y[0], y[1], y[2], y[3]), pack4_fp8(y[4], y[5], y[6], y[7]));
 }
 

@@ -142,3 +142,29 @@ def test_per_row_quantization_is_per_tensor_on_each_row():
     y = (x[0, 1].float() * 8.0).to(torch.bfloat16)
     cy, sy = O.quantize_fp8_per_row(O.bf16_tensor_bits(y)[None])
     assert np.array_equal(cy[0], codes[0, 1]) and sy[0] == np.float32(8.0) * scales[0, 1]
+
+
+def test_reciprocal_product_rounds_like_the_division():
+    """The device quantizer forms bf16(x / s) as bf16(x * r), r the correctly
+    rounded f32 reciprocal of s, with no near-tie fallback: x and s are both
+    bf16, so x / s is never within 2^-17 (relative) of a bf16 rounding tie
+    while x * r is within 2^-23 of x / s.  Checked here in f32 arithmetic
+    against the reference's f32 division for every finite bf16 x and every
+    16th bf16 scale the per-tensor rule can produce (amax clamped to 1e-12,
+    at most the bf16 maximum: s in [2.2e-15, 7.6e35]); the values beyond 448
+    clamp alike.  (Every scale, run once: no mismatch either.)"""
+    def bf16_rne(f):
+        u = f.view(np.uint32).astype(np.uint64)
+        u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFFFFFF
+        return ((u >> 16) << 16).astype(np.uint32).view(np.float32)
+
+    x = (np.arange(65536, dtype=np.uint32) << 16).view(np.float32)
+    x = x[np.isfinite(x)]
+    s_all = (np.arange(0x7F80, dtype=np.uint32) << 16).view(np.float32)
+    s_all = s_all[(s_all >= np.float32(2.2e-15)) & (s_all <= np.float32(7.6e35))]
+    with np.errstate(over="ignore"):
+        for s in s_all[::16]:
+            r = np.float32(1.0) / s
+            a = np.clip(bf16_rne((x * r).astype(np.float32)), -448, 448)
+            b = np.clip(bf16_rne((x / s).astype(np.float32)), -448, 448)
+            assert np.array_equal(a, b), float(s)
