@@ -143,7 +143,7 @@ __device__ __forceinline__ void wait_vmcnt_w(int w) {
 // the 2 wait states before it (the fragments come from LDS, P' and its scales
 // are built slots earlier), a result is read by VALU only 19 or more after it
 // (16-pass XDL), no VALU touches an accumulator in flight, and a dependent
-// chain on one accumulator needs none.  tests/test_mfma_hazards.py checks the
+// chain on one accumulator needs none.  tests/test_isa_rules.py checks the
 // built code object for both rules along every path.
 __device__ __forceinline__ void qk_first(v16f& d, const v8i& a, const v8i& b) {
   asm volatile("v_mfma_f32_32x32x64_f8f6f4 %0, %1, %2, 0" : "=&v"(d) : "v"(a), "v"(b));

@@ -267,7 +267,7 @@ def combine(batch: int, num_heads: int, ws: torch.Tensor, out: torch.Tensor, lse
 
 
 def decode_fwd(q, kv_data, kv_indptr, kv_indices, sm_scale, kv_mode="fp8", out=None, ws=None, q_seq_len=1,
-               return_lse=False, page_size=1, kv_last_page_lens=None, q_dtype="fp8"):
+               return_lse=False, page_size=1, kv_last_page_lens=None, q_dtype="fp8", lse=None):
     """Whole operator: FP8-quantize q, plan, decode, combine.
 
     q: bf16 [rows, H, 576], rows = sequences x q_seq_len (row i of a sequence
@@ -280,7 +280,9 @@ def decode_fwd(q, kv_data, kv_indptr, kv_indices, sm_scale, kv_mode="fp8", out=N
     cache): Q keeps its own precision, no per-tensor quantization.  q_dtype
     "fp8_row" (``mla_decode_fwd_rowq``; 16 heads, fp8 or mxfp4 cache): Q
     quantized per head row inside the decode, which for up to 256 query rows
-    also plans its own work (two launches per call).
+    also plans its own work (two launches per call).  ``out`` (bf16 [rows, H,
+    512]) and ``lse`` (f32 [rows, H], with ``return_lse``) may be passed in;
+    each is allocated here only when it is not.
     """
     if int(page_size) != 1:
         if kv_indices is None or kv_last_page_lens is None:
@@ -303,7 +305,14 @@ def decode_fwd(q, kv_data, kv_indptr, kv_indices, sm_scale, kv_mode="fp8", out=N
         ws = workspace(batch, num_heads, mode, q.device)
     if out is None:
         out = torch.empty((batch, num_heads, V_DIM), dtype=torch.bfloat16, device=q.device)
-    lse = torch.empty((batch, num_heads), dtype=torch.float32, device=q.device) if return_lse else None
+    elif out.dtype != torch.bfloat16 or tuple(out.shape) != (batch, num_heads, V_DIM) or not out.is_contiguous():
+        raise ValueError(f"out must be a contiguous bf16 [{batch}, {num_heads}, {V_DIM}] tensor")
+    if not return_lse:
+        lse = None
+    elif lse is None:
+        lse = torch.empty((batch, num_heads), dtype=torch.float32, device=q.device)
+    elif lse.dtype != torch.float32 or tuple(lse.shape) != (batch, num_heads) or not lse.is_contiguous():
+        raise ValueError(f"lse must be a contiguous f32 [{batch}, {num_heads}] tensor")
     routes = {"fp8": "mla_decode_fwd", "bf16": "mla_decode_fwd_a16w8", "fp8_row": "mla_decode_fwd_rowq"}
     if q_dtype not in routes:
         raise ValueError(f"q_dtype must be 'fp8' (a8w8: per-tensor Q quant), 'bf16' (a16w8) or 'fp8_row' "

@@ -23,6 +23,13 @@ custom_kernel routes each (batch, kv_len) to its fastest path
 ``auto_kv_mode``.  Without the key the route is a8w8 over the fp8 cache, the
 one the north-star tolerance (2e-2) holds for on every shape.
 There is no fallback: a missing library or an unsupported shape raises.
+
+The result lives in a buffer the operator keeps per (shape, device), as the
+reference's own output cache does (mixed-mla/submission.py:115, 346-351): the
+next call of the same shape on the same device overwrites it, so a caller that
+keeps a result past that call clones it.  The evaluation harness reads each
+result before the next call and then drops it (eval.py:243-248).  With the
+workspace cached the same way, a call in steady state allocates nothing.
 """
 from __future__ import annotations
 
@@ -52,6 +59,20 @@ def auto_kv_mode(num_heads: int, kv_data: dict) -> str:
     raise ValueError("kv_mode 'auto' needs the fp8 or (at 16 heads) the mxfp4 cache in kv_data")
 
 
+# (rows, heads, device, return_lse) -> (out, lse or None)
+_out_cache: dict = {}
+
+
+def _outputs(rows: int, heads: int, device: torch.device, return_lse: bool):
+    key = (rows, heads, device, return_lse)
+    bufs = _out_cache.get(key)
+    if bufs is None:
+        out = torch.empty((rows, heads, ops.V_DIM), dtype=torch.bfloat16, device=device)
+        lse = torch.empty((rows, heads), dtype=torch.float32, device=device) if return_lse else None
+        bufs = _out_cache[key] = (out, lse)
+    return bufs
+
+
 def custom_kernel(data: input_t) -> output_t:
     q, kv_data, qo_indptr, kv_indptr, config = data
     q_seq_len = int(config.get("q_seq_len", 1))
@@ -72,7 +93,9 @@ def custom_kernel(data: input_t) -> output_t:
     if qo_indptr is not None and qo_indptr.numel() != kv_indptr.numel():
         raise ValueError("qo_indptr and kv_indptr must both have batch + 1 entries")
     page_size = int(config.get("page_size", 1))
-    return ops.decode_fwd(q, kv_data, kv_indptr, kv_indices, sm_scale, kv_mode, q_seq_len=q_seq_len,
-                          return_lse=bool(config.get("return_lse", False)), page_size=page_size,
+    return_lse = bool(config.get("return_lse", False))
+    out, lse = _outputs(q.shape[0], num_heads, q.device, return_lse)
+    return ops.decode_fwd(q, kv_data, kv_indptr, kv_indices, sm_scale, kv_mode, out=out, q_seq_len=q_seq_len,
+                          return_lse=return_lse, page_size=page_size,
                           kv_last_page_lens=config.get("kv_last_page_lens"),
-                          q_dtype=q_dtype)
+                          q_dtype=q_dtype, lse=lse)

@@ -5,7 +5,7 @@
 
 Prints ONE JSON line.  ``value`` is the mean device time of one
 ``custom_kernel(data)`` call (Q quant + plan + decode + combine) in µs for the
-headline workload (BASELINE configs[1] = config 2 unless --config), timed with
+headline workload (config 5, the largest BASELINE config, unless --config), timed with
 HIP events on the stream the kernels run on.  Before every timed call a
 512 MiB buffer is rewritten so the KV cache comes from HBM, not from L2/MALL
 (the reference harness flushes L2 the same way, eval.py:235).  The timed
@@ -16,11 +16,12 @@ back-to-back launches over rotating copies of the cache that evict each other
 from L2/MALL, one pair of events around them) by its algorithmic bytes:
 T*(c_kv+4) KV + index bytes, the fp8 Q read and the bf16 output write.  ``cpu_baseline`` times the
 CPU oracle (the reference path restated: quantize Q, dequantize, fp32
-attention) on this host for every config (the whole config when it fits the
-per-config budget, else its leading sequences, scaled by token share).  Each
-config also carries the gather ceiling of its cache layout: the
-mla_probe_gather variants (the decode's KV gather with no compute) over the
-same rows, and the decode's fraction of it.
+attention) on this host over the whole of every config.  Each config also
+carries the gather ceiling of its cache layout: the fastest mla_probe_gather
+variant (the decode's KV gather with no compute) over the same rows, and the
+decode's fraction of it; where that probe is slower than the decode itself (a
+cache so small that the probe measures its own launch), no ceiling is
+reported.
 """
 from __future__ import annotations
 
@@ -39,6 +40,11 @@ HBM_PEAK_GBS = 8000.0
 FP8_PEAK_TFLOPS = 5000.0
 C_KV = {"fp8": 576, "mxfp4": 306, "mxfp4k_fp8v": 818}
 METRIC = "us per MLA decode call per config; achieved HBM TB/s and MFMA % of peak"
+# the decode kernel each (heads, kv_mode) of the BASELINE configs launches (indexed caches)
+KERNEL_NAMES = {(16, "fp8"): "decode_h16_kernel<0,0,true,0> (16 heads, fp8 cache)",
+                (16, "mxfp4"): "decode_h16_kernel<1,2,true,0> (16 heads, mxfp4 K = V)",
+                (128, "fp8"): "decode_h128_kernel<true,false> (128 heads, fp8 cache)",
+                (128, "mxfp4k_fp8v"): "decode_h128_kernel<true,true> (128 heads, mxfp4 K + fp8 V)"}
 
 
 def log(msg):
@@ -304,9 +310,14 @@ def time_config(cid, steps, warmup, flush_buf, probe=True):
         "bytes_alg_call": call_bytes, "bytes_alg_decode": dec_bytes, "flops_alg": flops,
         "wall_s": round(wall, 4),
     }
-    if gather is not None:
+    if gather is not None and gather["us"] < dec_mean:
         res["gather_ceiling"] = gather
         res["frac_of_gather_ceiling"] = round(gather["us"] / dec_mean, 4)
+    elif gather is not None:  # the probe is slower than the decode: launch-bound, no ceiling
+        res["gather_ceiling"] = None
+        res["gather_probe_note"] = (f"gather probe {gather['us']} us is slower than the decode "
+                                    f"({round(dec_mean, 3)} us): it measures its own launch, not a ceiling")
+        gather = None
     if inrow is not None:
         res["in_row_scales"] = {"us_decode_kernel_mean": round(inrow, 3),
                                 "decode_hbm_GBs": round(dec_bytes / (inrow * 1e-6) / 1e9, 1)}
@@ -352,8 +363,9 @@ def gather_probe_sweep(reps, ntok=1 << 20):
 
 
 def cpu_baseline(cid, data, budget_s):
-    """Oracle reference path on this host's CPU: the whole config when one run
-    fits the budget, else the leading sequences that do (scaled by token share)."""
+    """Oracle reference path on this host's CPU over the whole config (every
+    sequence, every token): runs are repeated while the budget lasts, at least
+    three and at most ten, and the median is reported."""
     import numpy as np
     import torch
 
@@ -372,42 +384,24 @@ def cpu_baseline(cid, data, budget_s):
     qbits = O.bf16_tensor_bits(q)
     threads = os.cpu_count() or 1
     torch.set_num_threads(threads)
+    caches = {}
+    if f8 is not None:
+        caches.update(fp8_codes=f8, fp8_scale=f8s)
+    if f4 is not None:
+        caches.update(fp4_packed=f4, fp4_scales=f4s)
 
-    def run(nb):
-        sub_ptr = indptr[: nb + 1]
-        rows = idx[: sub_ptr[-1]]
-        caches = {}
-        if f8 is not None:
-            caches.update(fp8_codes=f8[rows], fp8_scale=f8s)
-        if f4 is not None:
-            caches.update(fp4_packed=f4[rows], fp4_scales=f4s[rows])
-        t0 = time.perf_counter()
-        O.reference_path(qbits[:nb], mode, caches, sub_ptr, np.arange(sub_ptr[-1]), cfg["sm_scale"])
-        return time.perf_counter() - t0, int(sub_ptr[-1])
-
-    # probe with the first sequence, then take as many leading sequences as
-    # one run of about budget/3 allows (all of them when it fits)
-    one, tok1 = run(1)
-    per_tok = one / max(tok1, 1)
-    nb = 1
-    while nb < B and per_tok * indptr[nb + 1] <= budget_s / 3:
-        nb += 1
     ts = []
     t_end = time.perf_counter() + budget_s
     while len(ts) < 3 or (len(ts) < 10 and time.perf_counter() < t_end):
-        t, ntok = run(nb)
-        ts.append(t)
-        if time.perf_counter() > t_end and len(ts) >= 1:
-            break
+        t0 = time.perf_counter()
+        O.reference_path(qbits, mode, caches, indptr, idx, cfg["sm_scale"])
+        ts.append(time.perf_counter() - t0)
     ts.sort()
     med = ts[len(ts) // 2]
-    scale = T / max(ntok, 1)
-    full = nb == B
-    sample = (f"whole config ({B} sequences, {T} tokens)" if full else
-              f"first {nb}/{B} sequences ({ntok}/{T} tokens), scaled by token share x{scale:.2f}")
-    return {"value": round(med * scale * 1e6, 1), "unit": "us per call", "cores": threads, "kind": "port",
-            "sample": f"oracle reference path (quantize Q, dequantize KV, fp32 torch attention): {sample}; "
-                      f"median of {len(ts)} reps", "full": full}
+    return {"value": round(med * 1e6, 1), "unit": "us per call", "cores": threads, "kind": "port",
+            "sample": f"oracle reference path (quantize Q, dequantize the KV cache, fp32 torch attention): "
+                      f"whole config ({B} sequences, {T} tokens); median of {len(ts)} runs",
+            "full": True}
 
 
 def profile_decode(cids, reps):
@@ -575,10 +569,11 @@ def main(argv=None):
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", type=int, default=2, help="headline workload (BASELINE configs[1] = 2)")
+    ap.add_argument("--config", type=int, default=5, help="headline workload (default: config 5, the largest)")
     ap.add_argument("--only-headline", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-budget-s", type=float, default=6.0, help="CPU-baseline time budget per config")
+    ap.add_argument("--cpu-budget-s", type=float, default=10.0,
+                    help="CPU-baseline time per config (whole config; at least 3 runs)")
     ap.add_argument("--no-probe", action="store_true", help="skip the per-config gather ceiling")
     ap.add_argument("--gather-probe", action="store_true",
                     help="sweep the gather-ceiling probe variants instead (own JSON line)")
@@ -650,7 +645,7 @@ def main(argv=None):
         "roofline": {"bound": "hbm", "achieved": head["decode_hbm_GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": head["decode_hbm_frac"], "traffic": traffic,
                      "traffic_source_digest": traffic_src, "source_digest": source_digest(),
-                     "kernel": "decode (mla decode_h16/decode_h128)",
+                     "kernel": KERNEL_NAMES[(spec["num_heads"], spec["kv_mode"])],
                      "bytes_per_launch": head["bytes_alg_decode"], "avg_launch_us": head["us_decode_kernel_mean"]},
         "cpu_baseline": head.get("cpu_baseline"),
         "per_config": per,

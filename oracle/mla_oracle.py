@@ -89,24 +89,33 @@ def bf16_to_f32(bits: np.ndarray) -> np.ndarray:
 
 
 def f32_to_bf16(x: np.ndarray) -> np.ndarray:
-    """float32 -> bf16 bits, round to nearest, ties to even (finite inputs).
+    """float32 -> bf16 bits, round to nearest, ties to even.
 
-    Written as a neighbour comparison: the two bf16 candidates are the
-    truncation and the next value up; pick the closer, ties to the one whose
-    last mantissa bit is 0.
+    Finite inputs are rounded by a neighbour comparison on the magnitude: the
+    two bf16 candidates are the truncation and the next value up (2^128, i.e.
+    +inf, above the largest finite bf16), both exact in float64; the closer
+    one wins, a tie goes to the one whose last mantissa bit is 0, so values at
+    or past the midpoint below 2^128 overflow to inf.  +-inf map to +-inf and a
+    NaN to a quiet NaN of the same sign, explicitly (no arithmetic on them).
     """
     x = np.asarray(x, dtype=np.float32)
     u = x.view(np.uint32)
-    lo = (u >> 16).astype(np.uint32)
-    hi = lo + 1
+    sign = (u >> 16) & 0x8000
+    mag = u & 0x7FFFFFFF
+    finite = mag < 0x7F800000
+    lo = np.where(finite, mag >> 16, 0).astype(np.uint32)
+    e = (lo >> 7).astype(np.int64)
     vlo = (lo << 16).view(np.float32).astype(np.float64)
-    vhi = (hi << 16).view(np.float32).astype(np.float64)
-    xd = x.astype(np.float64)
-    dlo = np.abs(xd - vlo)
-    dhi = np.abs(vhi - xd)
+    gap = np.where(e == 0, 2.0 ** -133, np.ldexp(1.0, np.maximum(e, 1) - 134))  # one bf16 ulp at lo
+    vhi = vlo + gap
+    xd = np.where(finite, mag, 0).astype(np.uint32).view(np.float32).astype(np.float64)
+    dlo = xd - vlo
+    dhi = vhi - xd
     pick_hi = (dhi < dlo) | ((dhi == dlo) & ((lo & 1) == 1))
-    out = np.where(pick_hi, hi, lo)
-    return out.astype(np.uint16)
+    out = lo + pick_hi.astype(np.uint32)
+    nonfinite = np.where(mag > 0x7F800000, (mag >> 16) | 0x40, mag >> 16)  # inf stays inf; NaN stays quiet NaN
+    out = np.where(finite, out, nonfinite)
+    return (out | sign).astype(np.uint16)
 
 
 # ----------------------------------------------------------------------------
@@ -215,7 +224,9 @@ def quantize_fp8_with_scale(x_bits: np.ndarray, scale: float) -> np.ndarray:
     e4m3fn_rne(clamp(bf16(x / scale), -448, 448)).  With the whole buffer's
     scale this is what ``quantize_fp8`` writes for any subset of its rows."""
     xf = bf16_to_f32(np.asarray(x_bits, dtype=np.uint16))
-    y = bf16_to_f32(f32_to_bf16(xf / np.float32(scale)))
+    with np.errstate(over="ignore"):  # an f32 quotient past the range is +-inf, as torch's division gives
+        q = xf / np.float32(scale)
+    y = bf16_to_f32(f32_to_bf16(q))
     return f32_to_e4m3fn(np.clip(y, -FP8_MAX, FP8_MAX))
 
 

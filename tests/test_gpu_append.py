@@ -130,7 +130,7 @@ def test_decode_through_incrementally_built_cache(cuda, kv_mode):
     cfg = inputs.make_config(len(lens), heads, sum(lens), kv_mode, sm, kv_indices, max(lens))
     qd = q.cuda()
     qo = torch.arange(len(lens) + 1, dtype=torch.int32, device=cuda)
-    out_inc = custom_kernel((qd, cache.kv_data(), qo, kv_indptr, cfg))
+    out_inc = custom_kernel((qd, cache.kv_data(), qo, kv_indptr, cfg)).clone()
 
     whole = inputs.build_kv_data(kv_all.reshape(-1, 1, 576).cuda(), kv_mode)
     cfg_w = dict(cfg, kv_indices=None)

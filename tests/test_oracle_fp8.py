@@ -63,9 +63,32 @@ def test_f32_to_bf16_matches_torch():
     u = u[((u >> 23) & 0xFF) != 0xFF]  # finite
     ties = (rng.integers(0, 2 ** 16, 10000, dtype=np.uint32) << 16) | 0x8000
     x = np.concatenate([u, ties.astype(np.uint32)]).view(np.float32)
-    x = x[np.isfinite(x) & (np.abs(x) < 3.3e38)]
+    x = x[np.isfinite(x)]
     ref = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
     assert np.array_equal(O.f32_to_bf16(x), ref)
+
+
+def test_f32_to_bf16_overflow_edge_and_nonfinite():
+    """Every f32 from just below the largest finite bf16 up to the largest
+    finite f32 (the last 2^16 + 2^15 patterns, both signs): below the midpoint
+    to 2^128 they round to 0x7F7F, from it on to inf, as torch rounds them;
+    +-inf stay +-inf and NaN stays a NaN of its sign, with no floating-point
+    warning raised on the way."""
+    import warnings
+
+    top = np.arange(0x7F7F0000, 0x7F800000, dtype=np.uint32)
+    x = np.concatenate([top, top | 0x80000000]).view(np.float32)
+    special = np.array([np.inf, -np.inf, np.nan, -np.nan], dtype=np.float32)
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")
+        got = O.f32_to_bf16(x)
+        got_s = O.f32_to_bf16(special)
+    ref = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, ref)
+    assert (got == 0x7F80).sum() == (got == 0xFF80).sum() == 0x8000  # from the midpoint 0x7F7F8000 on
+    assert got_s[0] == 0x7F80 and got_s[1] == 0xFF80
+    assert (got_s[2] & 0x7FFF) > 0x7F80 and (got_s[3] & 0x7FFF) > 0x7F80
+    assert (got_s[2] >> 15) == (special.view(np.uint32)[2] >> 31)
 
 
 def test_scalar_divide_semantics_agree():

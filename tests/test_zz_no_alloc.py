@@ -62,3 +62,28 @@ def test_noalloc_rejects_oversized_shape(cuda):
     sc = torch.ones(1, dtype=torch.float32, device=cuda)
     with pytest.raises(_lib.MlaLibraryError, match="64|workspace"):
         ops.decode_fwd_noalloc(q, {"fp8": (fp8, sc)}, indptr, None, 0.1, "fp8")
+
+
+@pytest.mark.parametrize("heads,mode", [(16, "fp8"), (128, "fp8"), (128, "mxfp4k_fp8v")])
+def test_noalloc_replays_under_graph_capture(cuda, heads, mode):
+    """The no-alloc entry point captured in a HIP graph (after one eager call
+    on the device, which resolves the scratch address): every replay, with
+    eager work between replays, equals the eager result bit for bit."""
+    print(f"noalloc graph capture H={heads} mode={mode}", flush=True)
+    q, kv, indptr, idx, qb, caches = host_case([900, 40, 333], heads, mode, seed=71)
+    qd, kv_data, _, indptr_d, cfg = device_data(q, kv, indptr, idx, caches, mode, 0.0721)
+    args = (qd, kv_data, indptr_d, cfg["kv_indices"], cfg["sm_scale"], mode)
+    eager = ops.decode_fwd_noalloc(*args, out=torch.empty((3, heads, 512), dtype=torch.bfloat16, device=cuda))
+    torch.cuda.synchronize()
+    eager = eager.clone()
+    out = torch.empty_like(eager)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        ops.decode_fwd_noalloc(*args, out=out)
+    for rep in range(3):
+        out.fill_(rep + 1.0)  # eager work between replays
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {rep} differs from the eager call"
+    del g
