@@ -55,13 +55,17 @@
 // V half rows (dims 256h .. +255, rows of 272 bytes, at their bank floor for
 // the transpose reads, which then need one address register) in 4 half-pair
 // stages, fetched one pair after their K (each half one iteration before its
-// stage is needed); the 18 e8m0 bytes of each K row in 3 stages, one byte per
-// dword (byte DMAs), placed so that a lane's 9 scales of a tile are three LDS
-// reads.  Every DMA of a pair has its own slot, and every pair issues all of
+// stage is needed); the 18 e8m0 bytes of each K row in 3 stages as five dword
+// DMAs per pair (dword j of every row of the pair in plane j: bytes 4j .. 4j +
+// 3 for j < 4, bytes 14 .. 17 for j = 4), so a lane's 9 scales of a tile are
+// three LDS reads.  Every DMA of a pair has its own slot, and every pair issues all of
 // them (past the item's end they re-fetch its last row), so each wave's
 // outstanding-DMA count at the two barriers is a compile-time constant.  QK is
 // the scaled f8f6f4 MFMA with fp4 A (K, 4 VGPRs), the lane's e8m0 byte as A
-// scale, and fp8 Q^T in the order that pairs with the fp4 K layout.
+// scale (K step ks of lane half hh scales by byte 2ks + hh; the lanes of half 1
+// shift their scale dwords down a byte, so every lane's scale of step ks sits
+// at byte 2 (ks & 1) of dword ks >> 1, the byte the MFMA selects), and fp8 Q^T
+// in the order that pairs with the fp4 K layout.
 //
 // Behavioural reference: mixed-mla/asm_dumps/aiter_mla.py:149-470 (interface,
 // 128-head folding :318-353), TASK/reference.py:349-369 (numerics).
@@ -103,7 +107,8 @@ struct M128 {
   static constexpr int VST = 272;                 // fp8 V half row: 16 chunks + 1 of padding
   static constexpr int VSTAGE = 2 * HT * VST;     // 17 one-KiB windows
   static constexpr int NV = 4;                    // V half stages
-  static constexpr int SSTAGE = 2 * HT * 18 * 4;  // e8m0 bytes, one per dword: 18 256-byte windows
+  static constexpr int SPLANES = 5;               // e8m0 dwords per row (bytes 0-15, then 14-17)
+  static constexpr int SSTAGE = SPLANES * 2 * HT * 4;  // plane j: dword j of the pair's 64 rows
   static constexpr int NSL = 8;                   // slot stages (one per pair)
   static constexpr int OFF_V = NK * KSTAGE;
   static constexpr int OFF_S = OFF_V + NV * VSTAGE;
@@ -111,7 +116,7 @@ struct M128 {
   static constexpr int OFF_FLAG = OFF_SLOT + NSL * 256;
   static constexpr int LDS = OFF_FLAG + 16;
   static constexpr int OFF_Q = 2 * KSTAGE;        // Q (prologue): K stage 2 and the V stages
-  static_assert(KSTAGE == 19 * 1024 && VSTAGE == 17 * 1024 && SSTAGE == 18 * 256, "DMA windows");
+  static_assert(KSTAGE == 19 * 1024 && VSTAGE == 17 * 1024 && SSTAGE == 5 * 256, "DMA windows");
   static_assert(OFF_Q + 128 * kQKDim <= OFF_S, "Q staging stays clear of the e8m0 stages");
   static_assert(LDS <= 160 * 1024, "LDS");
 };
@@ -151,19 +156,26 @@ __device__ __forceinline__ void qk_first(v16f& d, const v8i& a, const v8i& b) {
 __device__ __forceinline__ void qk_acc(v16f& d, const v8i& a, const v8i& b) {
   asm volatile("v_mfma_f32_32x32x64_f8f6f4 %0, %1, %2, %0" : "+v"(d) : "v"(a), "v"(b));
 }
-// the same with fp4 A (4 VGPRs: 32 e2m1 values) at the lane's e8m0 scale sa
-// (byte 0), fp8 B at unit scale
+// the same with fp4 A (4 VGPRs: 32 e2m1 values) at the lane's e8m0 scale: byte
+// 0 (HI = false) or byte 2 (HI = true) of sa (the A scale's byte select is
+// op_sel[0] + 2 op_sel_hi[0]); fp8 B at unit scale
+template <bool HI>
 __device__ __forceinline__ void qk4_first(v16f& d, const v4i& a, const v8i& b, int sa) {
-  asm volatile(
-      "v_mfma_scale_f32_32x32x64_f8f6f4 %0, %1, %2, 0, %3, %4 op_sel_hi:[0,0,0] cbsz:4"
-      : "=&v"(d)
-      : "v"(a), "v"(b), "v"(sa), "v"(127));
+  if constexpr (HI)
+    asm volatile("v_mfma_scale_f32_32x32x64_f8f6f4 %0, %1, %2, 0, %3, %4 op_sel_hi:[1,0,0] cbsz:4"
+                 : "=&v"(d) : "v"(a), "v"(b), "v"(sa), "v"(127));
+  else
+    asm volatile("v_mfma_scale_f32_32x32x64_f8f6f4 %0, %1, %2, 0, %3, %4 op_sel_hi:[0,0,0] cbsz:4"
+                 : "=&v"(d) : "v"(a), "v"(b), "v"(sa), "v"(127));
 }
+template <bool HI>
 __device__ __forceinline__ void qk4_acc(v16f& d, const v4i& a, const v8i& b, int sa) {
-  asm volatile(
-      "v_mfma_scale_f32_32x32x64_f8f6f4 %0, %1, %2, %0, %3, %4 op_sel_hi:[0,0,0] cbsz:4"
-      : "+v"(d)
-      : "v"(a), "v"(b), "v"(sa), "v"(127));
+  if constexpr (HI)
+    asm volatile("v_mfma_scale_f32_32x32x64_f8f6f4 %0, %1, %2, %0, %3, %4 op_sel_hi:[1,0,0] cbsz:4"
+                 : "+v"(d) : "v"(a), "v"(b), "v"(sa), "v"(127));
+  else
+    asm volatile("v_mfma_scale_f32_32x32x64_f8f6f4 %0, %1, %2, %0, %3, %4 op_sel_hi:[0,0,0] cbsz:4"
+                 : "+v"(d) : "v"(a), "v"(b), "v"(sa), "v"(127));
 }
 __device__ __forceinline__ void drain_v(v16f& x) { asm volatile("s_nop 15\n\ts_nop 15" : "+v"(x)); }
 // PV: O^T += V^T . P'^T with an e8m0 scale on B (one per lane: its head), A at
@@ -274,8 +286,8 @@ struct H128Sched {
 // The two-cache mode's DMAs of pair q, one per pair slot, each window's slot
 // index read two slots before: V(q) half 0 (type 0) at slots 3 + 4m, half 1
 // (type 1) at 24 + 4m, K(q + 2) rows (type 2) at 5, 13, 22, 30, 38, their e8m0
-// bytes (type 3) at 9, 17, 26, 34, 42; window m of a type is the wave's
-// window w + 4m of the stage.  Half 0 goes into the stage freed at the
+// dwords (type 3, five windows: m = 0 on every wave, m = 1 on wave 0) at 9 and
+// 17; window m of a type is the wave's window w + 4m of the stage.  Half 0 goes into the stage freed at the
 // barrier that ends pair q - 1, half 1 into the one freed at slot 20; K and
 // e8m0 into the stage of pair q - 1, free since that barrier too.
 struct MixSched {
@@ -283,22 +295,22 @@ struct MixSched {
     return type == 0 ? 3 + 4 * m : type == 1 ? 24 + 4 * m : type == 2 ? (m < 2 ? 5 + 8 * m : 6 + 8 * m)
                                                                        : (m < 2 ? 9 + 8 * m : 10 + 8 * m);
   }
-  // 8 type + m of the DMA at pair slot s, or -1
+  // windows per stage: V 17, K 19, e8m0 5; wave w has window m iff w + 4m is one of them
+  static constexpr int windows(int type) { return type < 2 ? 17 : type == 2 ? 19 : M128::SPLANES; }
+  static constexpr bool has(int type, int m, int w) { return w + 4 * m < windows(type); }
+  // 8 type + m of the DMA at pair slot s (a window some wave has), or -1
   static constexpr int dma(int s) {
     for (int ty = 0; ty < 4; ++ty)
       for (int m = 0; m < 5; ++m)
-        if (at(ty, m) == s) return 8 * ty + m;
+        if (has(ty, m, 0) && at(ty, m) == s) return 8 * ty + m;
     return -1;
   }
   static constexpr int read(int s) {
     for (int ty = 0; ty < 4; ++ty)
       for (int m = 0; m < 5; ++m)
-        if (at(ty, m) - 2 == s) return 8 * ty + m;
+        if (has(ty, m, 0) && at(ty, m) - 2 == s) return 8 * ty + m;
     return -1;
   }
-  // windows per stage: V 17, K 19, e8m0 18; wave w has the fifth (m = 4) iff
-  // w + 16 is one of them
-  static constexpr bool has(int type, int m, int w) { return m < 4 || w < (type < 2 ? 1 : type == 2 ? 3 : 2); }
   // DMAs wave w issues at pair slots [lo, hi) (with the slot-index DMA of wave 0)
   static constexpr int issued(int w, bool idx, int lo, int hi) {
     int c = (idx && w == 0 && lo <= H128Sched::kSlotDma && H128Sched::kSlotDma < hi) ? 1 : 0;
@@ -312,6 +324,12 @@ struct MixSched {
   // landed: V(q - 1) half 1, K(q + 1), e8m0(q + 1))
   static constexpr int left_free(int w, bool idx) { return issued(w, idx, 20, 50) + issued(w, idx, 0, 20); }
   static constexpr int left_pub(int w, bool idx) { return issued(w, idx, 43, 50) + issued(w, idx, 0, 45); }
+  // K and e8m0 windows of one pair that wave w issues
+  static constexpr int ks_per_pair(int w) {
+    int c = 0;
+    for (int m = 0; m < 5; ++m) c += (has(2, m, w) ? 1 : 0) + (has(3, m, w) ? 1 : 0);
+    return c;
+  }
   static_assert(H128Sched::kStageFree == 20 && H128Sched::kBarrier == 45, "barrier slots");
 };
 
@@ -408,9 +426,9 @@ __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams 
   // Two-cache mode: window m of each type (the wave's window u = w + 4m of the
   // stage) puts lane l at position e = 64u + l: K, chunk e of the stage = row
   // e / 19, chunk e % 19 (the padding chunk re-fetches chunk 0); V half, row e /
-  // 17, chunk e % 17 (likewise); e8m0, dword e = row r, byte 2ks + hh at 16r +
-  // 8hh + ks (ks < 8), byte 16 + hh at 1024 + 64hh + r.  Packed (r << 9 | source
-  // byte offset in the row), entries K 0..4, e8m0 5..9, V 10..14.
+  // 17, chunk e % 17 (likewise); e8m0, plane u, row l: the dword at byte 4u (u <
+  // 4) or 14 (u = 4) of the row's scales.  Packed (r << 9 | source byte offset
+  // in the row), entries K 0..4, e8m0 5..9, V 10..14.
   constexpr int kMaps = MIX ? 8 : G128::DMAX / 2;
   uint32_t dmap[kMaps];
   if constexpr (MIX) {
@@ -420,10 +438,8 @@ __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams 
       const int e = 64 * (w + 4 * m) + lane;
       const int rk = min(e / 19, 63), ck = e - 19 * (e / 19);
       ent[m] = ((uint32_t)rk << 9) | (uint32_t)(16 * (ck < 18 ? ck : 0));
-      const int e2 = e - 1024;
-      const int rs_ = e < 1024 ? e >> 4 : e2 & 63;
-      const int js = e < 1024 ? 2 * (e & 7) + ((e >> 3) & 1) : 16 + ((e2 >> 6) & 1);
-      ent[5 + m] = ((uint32_t)rs_ << 9) | (uint32_t)js;
+      const int u = w + 4 * m;
+      ent[5 + m] = u < M128::SPLANES ? ((uint32_t)lane << 9) | (uint32_t)(u < 4 ? 4 * u : 14) : 0u;
       const int rv = min(e / 17, 63), cv = e - 17 * (e / 17);
       ent[10 + m] = ((uint32_t)rv << 9) | (uint32_t)(16 * (cv < 16 ? cv : 0));
     }
@@ -519,7 +535,7 @@ __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams 
         const uint8_t* src = p.k_scales + ((uint64_t)(uint32_t)sl * (uint32_t)p.k_scale_stride + off);
         uint32_t saved;
         asm volatile("s_mov_b32 %0, m0\n\ts_add_u32 m0, %1, %2\n\ts_mov_b32 %0, %0\n\t"
-                     "global_load_lds_ubyte %3, off\n\ts_mov_b32 m0, %0"
+                     "global_load_lds_dword %3, off\n\ts_mov_b32 m0, %0"
                      : "=&s"(saved)
                      : "s"(base), "i"(1024 * m), "v"(src)
                      : "memory", "scc");
@@ -564,9 +580,8 @@ __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams 
   // ka[2 (ks & 1) + j] + 128 (ks >> 1) (ks < 8), ka[4 + j] (ks = 8): LDS
   // addresses of the current K tile, moved along the ring in place.
   // Two-cache mode.  K fragment of step ks: chunk 2ks + hh of row l32 of the
-  // tile, at ka[0] + 32ks; the tile's e8m0 bytes: ks < 8 at ka[1] + 4ks (two
-  // 16-byte reads), ks = 8 at ka[2].
-  uint32_t ka[MIX ? 3 : 6];
+  // tile, at ka[0] + 32ks; the row's e8m0 dword j at ka[1] + 256j.
+  uint32_t ka[MIX ? 2 : 6];
   // (the init lambdas derive everything from an opaque copy of the lane id, so
   // the addresses are formed where they are needed, not kept live from the entry)
   auto init_ka = [&]() __attribute__((always_inline)) {
@@ -575,8 +590,7 @@ __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams 
     if constexpr (MIX) {  // pair 0: stage 0, tile 0
       const int r = ln & 31, h = ln >> 5;
       ka[0] = lds0 + r * M128::KST + 16 * h;
-      ka[1] = lds0 + M128::OFF_S + 64 * r + 32 * h;
-      ka[2] = lds0 + M128::OFF_S + 4096 + 256 * h + 4 * r;
+      ka[1] = lds0 + M128::OFF_S + 4 * r;
     } else {
       const int r = ln & 31, h2 = (ln >> 5) * 2, x = g128_key(r);
 #pragma unroll
@@ -620,8 +634,11 @@ __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams 
   typedef __attribute__((address_space(3))) int lds_i32;
   v8i kf[3];
   v4i kf4[3];                  // two-cache mode: fp4 K fragments
-  v4i sc_lo, sc_hi;            // two-cache mode: e8m0 of steps 0..3, 4..7
-  int sc8 = 127;               // and of step 8
+  // two-cache mode: e8m0 dwords of the K tile (steps 0..3, 4..7, 8), each
+  // shifted down by 8 hh once loaded (byte 2 (ks & 1) of dword ks >> 1, byte 2 of sc8)
+  int sc_lo[2] = {0x7F7F7F7F, 0x7F7F7F7F}, sc_hi[2] = {0x7F7F7F7F, 0x7F7F7F7F};
+  int sc8 = 0x7F7F7F7F;
+  const int sc_shift = 8 * hh;
   auto kload = [&](int g) __attribute__((always_inline)) {  // K fragment of step g (0..8) into kf[g % 3]
     if constexpr (MIX) {
       kf4[g % 3] = *(const lds_v4i*)(uintptr_t)(ka[0] + 32 * g);
@@ -653,10 +670,31 @@ __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams 
       vf[g % 2] = v8i{r0[0], r0[1], r1[0], r1[1], r2[0], r2[1], r3[0], r3[1]};
     }
   };
-  // two-cache mode: the e8m0 bytes of the current K tile (ka[1], ka[2])
-  auto scload_lo = [&]() __attribute__((always_inline)) { sc_lo = *(const lds_v4i*)(uintptr_t)ka[1]; };
-  auto scload_hi = [&]() __attribute__((always_inline)) { sc_hi = *(const lds_v4i*)(uintptr_t)(ka[1] + 16); };
-  auto scload_8 = [&]() __attribute__((always_inline)) { sc8 = *(const lds_i32*)(uintptr_t)ka[2]; };
+  // two-cache mode: the e8m0 dwords of the current K tile (ka[1]), and their
+  // per-lane-half shift (a separate step, placed slots after the read)
+  auto scload_lo = [&]() __attribute__((always_inline)) {
+    sc_lo[0] = *(const lds_i32*)(uintptr_t)ka[1];
+    sc_lo[1] = *(const lds_i32*)(uintptr_t)(ka[1] + 256);
+  };
+  auto scload_hi = [&]() __attribute__((always_inline)) {
+    sc_hi[0] = *(const lds_i32*)(uintptr_t)(ka[1] + 512);
+    sc_hi[1] = *(const lds_i32*)(uintptr_t)(ka[1] + 768);
+  };
+  auto scload_8 = [&]() __attribute__((always_inline)) { sc8 = *(const lds_i32*)(uintptr_t)(ka[1] + 1024); };
+  // (asm, so that the shift stays in its slot: a plain shift is a value the
+  // compiler may recompute right before its MFMA, inside the wait states)
+  auto shr = [&](int& x) __attribute__((always_inline)) {
+    asm volatile("v_lshrrev_b32 %0, %1, %0" : "+v"(x) : "v"(sc_shift));
+  };
+  auto scshift_lo = [&]() __attribute__((always_inline)) {
+    shr(sc_lo[0]);
+    shr(sc_lo[1]);
+  };
+  auto scshift_hi = [&]() __attribute__((always_inline)) {
+    shr(sc_hi[0]);
+    shr(sc_hi[1]);
+  };
+  auto scshift_8 = [&]() __attribute__((always_inline)) { shr(sc8); };
   // two-cache mode: outstanding-DMA waits of the two barriers
   auto mix_wait_free = [&]() __attribute__((always_inline)) {
     wait_vmcnt_w<MS::left_free(0, IDX), MS::left_free(1, IDX), MS::left_free(2, IDX), MS::left_free(3, IDX)>(w);
@@ -798,9 +836,10 @@ __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams 
         constexpr int g = i / 3;
         if (KQ == 1 || t < n) {
           if constexpr (MIX) {
-            const int sa = g < 4 ? sc_lo[g & 3] : g < 8 ? sc_hi[g & 3] : sc8;
-            if constexpr (g == 0) qk4_first(s_qk, kf4[0], qv[0], sa);
-            else qk4_acc(s_qk, kf4[g % 3], qv[g], sa);
+            const int sa = g < 4 ? sc_lo[(g >> 1) & 1] : g < 8 ? sc_hi[(g >> 1) & 1] : sc8;
+            constexpr bool HI = g == 8 || (g & 1) != 0;  // byte 2 (odd steps, step 8), else byte 0
+            if constexpr (g == 0) qk4_first<HI>(s_qk, kf4[0], qv[0], sa);
+            else qk4_acc<HI>(s_qk, kf4[g % 3], qv[g], sa);
           } else {
             if constexpr (g == 0) qk_first(s_qk, kf[0], qv[0]);
             else qk_acc(s_qk, kf[g % 3], qv[g]);
@@ -861,10 +900,15 @@ __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams 
       }
       // 4. fragment loads, address moves
       if constexpr (SC::kload(i) >= 0) kload(SC::kload(i) % 9);
-      if constexpr (MIX) {  // e8m0: steps 0..7 of the next tile once its QK is past them, step 8 after
+      if constexpr (MIX) {  // e8m0: steps 0..7 of the next tile once its QK is past them, step 8 after;
+        // each shifted two to four slots after its read, and two or more MFMA
+        // slots before its first MFMA (steps 0, 4 and 8: slots 0, 12, 24)
         if constexpr (i == 20) scload_lo();
+        if constexpr (i == 22) scshift_lo();
         if constexpr (i == 22) scload_hi();
         if constexpr (i == 1) scload_8();
+        if constexpr (i == 2) scshift_hi();
+        if constexpr (i == 5) scshift_8();
       }
       if constexpr (SC::vload(i) >= 0) {
         constexpr int g = SC::vload(i);
@@ -875,13 +919,11 @@ __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams 
         if constexpr (MIX) {  // K and e8m0 tiles: + 32 rows, or on to the next pair's stage
           const int step = (q % 3 == 2) ? -2 : 1;
           const int dk = IT == 0 ? 32 * M128::KST : step * M128::KSTAGE - 32 * M128::KST;
-          const int ds = IT == 0 ? 2048 : step * M128::SSTAGE - 2048;
-          const int d8 = IT == 0 ? 128 : step * M128::SSTAGE - 128;
+          const int ds = IT == 0 ? 32 * 4 : step * M128::SSTAGE - 32 * 4;
           ka[0] += dk;
           ka[1] += ds;
-          ka[2] += d8;
 #pragma unroll
-          for (int jj = 0; jj < 3; ++jj) asm volatile("" : "+v"(ka[jj]));
+          for (int jj = 0; jj < 2; ++jj) asm volatile("" : "+v"(ka[jj]));
         } else {
           const int dk = IT == 0 ? G128::TSTAGE : (((q + 1) & 3) - (q & 3)) * G128::PSTAGE - G128::TSTAGE;
 #pragma unroll
@@ -957,11 +999,12 @@ __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams 
       issue_slots(3);
       if constexpr (MIX) mix_issue_ks(1);
       else issue_rows(1);
-      // two-cache mode: K and e8m0 windows of a pair per wave, 5 + 5, 5 + 5, 5 + 4, 4 + 4
+      // two-cache mode: K and e8m0 windows of a pair per wave (MS::ks_per_pair)
       constexpr int S0 = IDX ? 1 : 0;
       if (first) {  // this wave's Q rows landed (issued before the DMAs since)
         if constexpr (MIX) {
-          wait_vmcnt_w<2 * S0 + 20, 20, 18, 16>(w);
+          wait_vmcnt_w<2 * S0 + 2 * MS::ks_per_pair(0), 2 * MS::ks_per_pair(1), 2 * MS::ks_per_pair(2),
+                       2 * MS::ks_per_pair(3)>(w);
         } else {
           if (w == 0) wait_vmcnt<IDX ? 2 * G128::DMAX + 2 : 2 * G128::DMAX>();
           else if (w == 1) wait_vmcnt<2 * G128::DMAX>();
@@ -969,17 +1012,20 @@ __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams 
         }
         read_q();
       }
-      if constexpr (MIX) wait_vmcnt_w<S0 + 10, 10, 9, 8>(w);  // K and e8m0 of pair 0
+      if constexpr (MIX)  // K and e8m0 of pair 0
+        wait_vmcnt_w<S0 + MS::ks_per_pair(0), MS::ks_per_pair(1), MS::ks_per_pair(2), MS::ks_per_pair(3)>(w);
       else wait_rows();
       lds_barrier();  // pair 0 visible; every wave's Q^T reads done (its stages reusable)
       init_ka();
       init_va();
       kload(0);
       kload(1);
-      if constexpr (MIX) {
+      if constexpr (MIX) {  // tile 0's steps 0..3 (shifted here), 4..7 (shifted at slot 2); step 8 at slot 1
         scload_lo();
         scload_hi();
-        scload_8();
+        scshift_lo();
+        // the shifted dwords are MFMA sources: two wait states before the first QK
+        asm volatile("s_nop 1" : "+v"(sc_lo[0]), "+v"(sc_lo[1]));
       }
       vload(1, 0);
       // pairs: the first two (pipeline fill), the steady ones (every part of
