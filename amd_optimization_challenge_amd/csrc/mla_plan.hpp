@@ -35,6 +35,7 @@ __device__ __forceinline__ int row_len(const int32_t* __restrict__ kv_indptr, in
 struct WavePlan {
   int n_items, chunk;
   int first, nb;
+  int s0_b, len_b;  // lane b's own row: first key, key count
   int x, nb_r, seq_r, s0_r, len_r;
   unsigned hi64, lo64;
 };
@@ -111,6 +112,8 @@ __device__ __forceinline__ WavePlan plan_wave(const int32_t* __restrict__ kv_ind
   P.seq_r = __builtin_amdgcn_ds_permute(rank << 2, lane);
   P.s0_r = __builtin_amdgcn_ds_permute(rank << 2, s0);
   P.len_r = __builtin_amdgcn_ds_permute(rank << 2, L);
+  P.s0_b = s0;
+  P.len_b = L;
   return P;
 }
 

@@ -296,19 +296,17 @@ __device__ __forceinline__ void emit_pieces(int4* __restrict__ items, int b, int
   }
 }
 
-// Up to 64 rows: one wave plans alone (mla_plan.hpp) and writes the items in
-// parallel, lane i taking items i, i + 64, ...
+// Up to 64 rows: one wave plans alone (mla_plan.hpp); lane b writes row b's
+// pieces (emit_pieces: the bounds plan_wave_item gives, by a running
+// remainder), a few stores per lane instead of a search per item
 __device__ __forceinline__ void build_plan_wave(const int32_t* __restrict__ kv_indptr, int batch, int qlen,
                                                 int target_items, int min_chunk, int max_splits, int max_items,
                                                 int32_t* __restrict__ plan) {
   const WavePlan P = plan_wave(kv_indptr, batch, qlen, target_items, min_chunk, max_splits);
   plan_wave_write_rows(P, batch, max_items, plan);
   int4* items = reinterpret_cast<int4*>(plan + kPlanHeader);
-  for (int base = 0; base < P.n_items; base += 64) {
-    const int i = base + (int)(threadIdx.x & 63);
-    const int4 it = plan_wave_item(P, i);
-    if (i < P.n_items) items[i] = it;
-  }
+  const int b = (int)(threadIdx.x & 63);
+  if (b < batch) emit_pieces(items, b, P.s0_b, P.len_b, P.nb, P.first);
 }
 
 __device__ __forceinline__ void build_plan(const int32_t* __restrict__ kv_indptr, int batch, int qlen,
