@@ -248,7 +248,8 @@ int mla_decode_fwd_rowq(const void* q_bf16, const void* k_cache, int64_t k_row_s
  * mla_workspace_bytes exceeds it returns MLA_ERR_WORKSPACE_TOO_SMALL.  Calls
  * on one device share that array: calls that overlap on a device (other
  * streams, other threads) race; calls ordered on one stream do not.  It calls
- * no allocator.
+ * no allocator.  The first call on a device resolves the array's address
+ * (hipGetSymbolAddress): make it eagerly before capturing a call in a graph.
  */
 int mla_decode_fwd_noalloc(const void* q_bf16, const void* k_cache, int64_t k_row_stride,
                            const void* k_scales, int64_t k_scale_stride, const void* v_cache,
