@@ -361,8 +361,9 @@ __global__ __launch_bounds__(256, 1) void decode_h128_kernel(const DecodeParams 
   // the plan has room for max_items >= gridDim.x items)
   const int32_t* plan = p.plan;
   const int nitems = plan[0];
-  const int4 it = reinterpret_cast<const int4*>(plan + kPlanHeader)[blockIdx.x];
-  if ((int)blockIdx.x >= nitems) return;
+  const int item = xcd_item<2>((int)blockIdx.x, (int)gridDim.x);  // a row's pieces, and its Q, share an L2
+  const int4 it = reinterpret_cast<const int4*>(plan + kPlanHeader)[item];
+  if (item >= nitems) return;
   const int b = it.x, t_beg = it.y, t_end = it.z, slot = it.w;
   const int ntok = t_end - t_beg;
   const int n = (ntok + C::HT - 1) / C::HT;  // 32-token tiles

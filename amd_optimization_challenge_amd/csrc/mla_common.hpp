@@ -306,6 +306,22 @@ __device__ __forceinline__ int wave_max(int x) { return __builtin_amdgcn_readlan
 
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// Work-group g of a launch runs on XCD g % 8: the dispatcher deals
+// work-groups out round-robin over the 8 XCDs, each with its own L2.  Plan
+// items of one query row are consecutive and read the same Q, so items go to
+// XCDs M at a time: in each block of 8M work-groups, those of XCD x (g = x,
+// x + 8, ..) take items xM .. xM + M - 1.  A partial last block keeps the
+// identity, so this is a bijection on [0, G); a block of 8M work-groups that
+// divides the CU count keeps every item in the dispatch round it had.
+template <int M>
+__device__ __forceinline__ int xcd_item(int g, int G) {
+  static_assert(M > 0 && (M & (M - 1)) == 0, "M is a power of two");
+  const int base = g & ~(8 * M - 1);
+  if (base + 8 * M > G) return g;
+  const int r = g - base;
+  return base + (r & 7) * M + (r >> 3);
+}
+
 // ds_read_b64_tr_b8: within each 16-lane group, result lane j gets byte (j & 7)
 // of the 8-byte reads of lanes 2m + (j >> 3), m = 0..7, in that order.
 typedef int v2i __attribute__((ext_vector_type(2)));

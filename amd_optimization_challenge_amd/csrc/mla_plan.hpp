@@ -210,55 +210,134 @@ __device__ __forceinline__ int block_exscan(int v, int* red, int* total) {
 // call it): the block form of the plan, which the planner kernel uses above
 // 64 rows and the 16-head decode for up to 256.  Thread b < batch gets row
 // b's length, piece count, first key and first item; every thread gets the
-// chunk, the item count and the length sums.  Scratch: 256 keys, 256 counts
-// and 4 ints of LDS; it ends with a barrier after its last scratch read.
+// chunk, the item count and the length sums.  Scratch: 256 keys (8 bytes
+// each), 256 counts and kPlanRedInts ints of LDS; it ends with a barrier after
+// its last scratch read.  The chunk is the one-wave plan's (the same search
+// bounds, the same closed form for equal lengths), found four candidates a
+// round; each reduction round is one barrier, its partials in one of two
+// banks of s_red that alternate, so a bank is rewritten only after every
+// thread has passed the barrier that follows its reads.
 struct BlockPlan {
   int chunk, n_items;
   unsigned hi64, lo64;
   int L, nb, s0, first;
 };
+constexpr int kPlanRedInts = 64;
 __device__ __forceinline__ BlockPlan plan_block(const int32_t* __restrict__ kv_indptr, int batch, int qlen,
                                                 int target_items, int min_chunk, int max_splits,
                                                 uint64_t* s_key, int* s_cnt, int* s_red) {
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const bool act = tid < batch;
   BlockPlan P;
   P.L = act ? row_len(kv_indptr, tid, qlen) : 0;
   P.s0 = act ? row_start(kv_indptr, tid, qlen) : 0;
-  P.hi64 = (unsigned)block_sum(P.L >> 6, s_red);
-  P.lo64 = (unsigned)block_sum(P.L & 63, s_red);
-  const int lmax = block_max(P.L, s_red);
-  int chunk = 64 * max(min_chunk / 64, (int)tiles_per_item(P.hi64, P.lo64, target_items));
-  if (max_splits > 0) chunk = max(chunk, 64 * (((lmax + 63) / 64 + max_splits - 1) / max_splits));
-  // binary search on chunk / 64 in [c0 / 64, ceil(lmax / 64)]
   const int L64 = (P.L + 63) >> 6;
-  int lo = chunk / 64, hi = max(lo, (lmax + 63) / 64);
+  // round 1 (bank 0): sums of L >> 6, L & 63 and ceil(L / 64), max of L, min of ceil(L / 64)
+  {
+    const int a0 = wave_sum(P.L >> 6), a1 = wave_sum(P.L & 63), a2 = wave_max(P.L), a3 = wave_sum(L64);
+    const int a4 = wave_max(act ? -L64 : -0x7FFFFFFF);
+    if (lane == 0) {
+      s_red[w] = a0;
+      s_red[4 + w] = a1;
+      s_red[8 + w] = a2;
+      s_red[12 + w] = a3;
+      s_red[16 + w] = a4;
+    }
+  }
+  __syncthreads();
+  P.hi64 = (unsigned)(s_red[0] + s_red[1] + s_red[2] + s_red[3]);
+  P.lo64 = (unsigned)(s_red[4] + s_red[5] + s_red[6] + s_red[7]);
+  const int lmax = max(max(s_red[8], s_red[9]), max(s_red[10], s_red[11]));
+  const unsigned s64 = (unsigned)(s_red[12] + s_red[13] + s_red[14] + s_red[15]);
+  const int l64min = -max(max(s_red[16], s_red[17]), max(s_red[18], s_red[19]));
+  int lo = max(min_chunk / 64, (int)tiles_per_item(P.hi64, P.lo64, target_items));
+  if (max_splits > 0) lo = max(lo, ((lmax + 63) / 64 + max_splits - 1) / max_splits);
+  // m = ceil(s64 / (target - batch)) already fits (at most s64 / m + batch items)
+  int hi = (lmax + 63) / 64;
+  if (target_items > batch)
+    hi = min(hi, (int)((s64 + (unsigned)(target_items - batch) - 1u) / (unsigned)(target_items - batch)));
+  hi = max(lo, hi);
+  if (l64min == (lmax + 63) / 64) {  // every row as long: the count at m is batch ceil(L64 / m)
+    const int k = target_items / max(batch, 1);
+    lo = hi = k > 0 ? min(hi, max(lo, (l64min + k - 1) / k)) : hi;
+  }
+  // smallest m in [lo, hi) whose item count fits the target (else hi): the
+  // count is non-increasing in m; three probes a round keep the answer in [lo, hi]
+  int bank = 1;
   while (lo < hi) {
-    const int mid = (lo + hi) >> 1;
-    const int cnt = block_sum(act ? (L64 > 0 ? (L64 + mid - 1) / mid : 1) : 0, s_red);
-    if (cnt <= target_items) hi = mid;
-    else lo = mid + 1;
+    const int d = hi - lo;
+    const int m1 = lo + d / 4, m2 = lo + d / 2, m3 = lo + (3 * d) / 4;
+    auto cnt = [&](int m) { return act ? (L64 > 0 ? (L64 + m - 1) / m : 1) : 0; };
+    const int c1 = wave_sum(cnt(m1)), c2 = wave_sum(cnt(m2)), c3 = wave_sum(cnt(m3));
+    int* rb = s_red + 32 * bank;
+    if (lane == 0) {
+      rb[w] = c1;
+      rb[4 + w] = c2;
+      rb[8 + w] = c3;
+    }
+    __syncthreads();
+    const int n1 = rb[0] + rb[1] + rb[2] + rb[3], n2 = rb[4] + rb[5] + rb[6] + rb[7];
+    const int n3 = rb[8] + rb[9] + rb[10] + rb[11];
+    if (n1 <= target_items) {
+      hi = m1;
+    } else if (n2 <= target_items) {
+      lo = m1 + 1;
+      hi = m2;
+    } else if (n3 <= target_items) {
+      lo = m2 + 1;
+      hi = m3;
+    } else {
+      lo = m3 + 1;
+    }
+    bank ^= 1;
   }
   P.chunk = lo * 64;
   P.nb = act ? (P.L > 0 ? (P.L + P.chunk - 1) / P.chunk : 1) : 0;
   // rank rows by piece length, longest first (ties by index); equal pieces on
-  // every row leave them in index order.  Otherwise key = piece << 32 |
-  // (2^32 - 1 - b): a larger key ranks earlier, and "no row" is key 0, below
-  // every real one; two keys per 16-byte LDS read, one compare each.
+  // every row leave them in index order
   const int piece = act ? (P.L > 0 ? (P.L + P.nb - 1) / P.nb : 0) : -1;
-  const int pmax = block_max(act ? piece : 0, s_red), npmin = block_max(act ? -piece : -0x7FFFFFFF, s_red);
+  {
+    const int a0 = wave_max(act ? piece : 0), a1 = wave_max(act ? -piece : -0x7FFFFFFF);
+    int* rb = s_red + 32 * bank;
+    if (lane == 0) {
+      rb[w] = a0;
+      rb[4 + w] = a1;
+    }
+  }
+  __syncthreads();
+  const int* rp = s_red + 32 * bank;
+  const int pmax = max(max(rp[0], rp[1]), max(rp[2], rp[3]));
+  const int npmin = max(max(rp[4], rp[5]), max(rp[6], rp[7]));
   int rank = tid;
   if (pmax != -npmin) {
-    const uint64_t key = piece < 0 ? 0ull : ((uint64_t)(uint32_t)piece << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)tid);
-    s_key[tid] = key;
-    __syncthreads();
     rank = 0;
-    if (act) {
-      const ulonglong2* kv = reinterpret_cast<const ulonglong2*>(s_key);
+    if (pmax < (1 << 23)) {
+      // key = (piece + 1) 256 + 255 - b: a larger key ranks earlier, "no row"
+      // is 0, below every real one; four keys per 16-byte LDS read
+      uint32_t* k32 = reinterpret_cast<uint32_t*>(s_key);
+      const uint32_t key = act ? ((uint32_t)(piece + 1) << 8) | (uint32_t)(255 - tid) : 0u;
+      k32[tid] = key;
+      __syncthreads();
+      if (act) {
+        const uint4* kv = reinterpret_cast<const uint4*>(k32);
 #pragma unroll 8
-      for (int b2 = 0; b2 < (batch + 1) / 2; ++b2) {
-        const ulonglong2 q = kv[b2];
-        rank += (q.x > key) + (q.y > key);
+        for (int b2 = 0; b2 < (batch + 3) / 4; ++b2) {
+          const uint4 q = kv[b2];
+          rank += (q.x > key) + (q.y > key) + (q.z > key) + (q.w > key);
+        }
+      }
+    } else {
+      // key = piece << 32 | (2^32 - 1 - b), two per 16-byte LDS read
+      const uint64_t key = piece < 0 ? 0ull : ((uint64_t)(uint32_t)piece << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)tid);
+      s_key[tid] = key;
+      __syncthreads();
+      if (act) {
+        const ulonglong2* kv = reinterpret_cast<const ulonglong2*>(s_key);
+#pragma unroll 8
+        for (int b2 = 0; b2 < (batch + 1) / 2; ++b2) {
+          const ulonglong2 q = kv[b2];
+          rank += (q.x > key) + (q.y > key);
+        }
       }
     }
   }
