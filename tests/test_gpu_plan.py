@@ -20,6 +20,11 @@ CASES = [
     [(i * 7919) % 9000 + 1 for i in range(65)],
     [(i * 104729) % 33000 for i in range(256)],
     [(i * 37) % 2000 for i in range(257)],
+    # the block planner's closed form (every row as long) and its 64-bit rank
+    # keys (a piece of 2^23 tokens or more: at 128 heads, 200 rows share 256
+    # items, so the 5e8-token row is cut into at most 57 pieces)
+    [777] * 100,
+    [500_000_000] + [(i * 37) % 2000 + 1 for i in range(199)],
 ]
 
 
@@ -55,8 +60,16 @@ def expected_chunk(lens, target, min_chunk, max_splits):
         c0 = max(c0, 64 * -(-(-(-max(lens) // 64)) // max_splits))
     count = lambda c: sum(max(1, -(-L // c)) for L in lens)
     if len(lens) <= 256:
-        cands = [c for c in range(c0, max(c0, -(-max(lens) // 64) * 64) + 1, 64) if count(c) <= target]
-        return cands[0] if cands else max(c0, -(-max(lens) // 64) * 64)
+        # the smallest multiple of 64 in [c0, top] whose count fits (the count
+        # is non-increasing in c), else top
+        lo, hi = c0 // 64, max(c0, -(-max(lens) // 64) * 64) // 64
+        while lo < hi:
+            mid = (lo + hi) // 2
+            if count(64 * mid) <= target:
+                hi = mid
+            else:
+                lo = mid + 1
+        return 64 * lo
     return c0
 
 
