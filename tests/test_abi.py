@@ -12,7 +12,8 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
 def declared_symbols():
-    text = open(os.path.join(ROOT, "include", "mla_mi355x.h")).read()
+    with open(os.path.join(ROOT, "include", "mla_mi355x.h")) as f:
+        text = f.read()
     return sorted(set(re.findall(r"^\s*(?:const\s+char\s*\*|int64_t|int)\s+(mla_\w+)\s*\(", text, re.M)))
 
 
