@@ -3,6 +3,7 @@
     python -m amd_optimization_challenge_amd.profsum trace  <p_kernel_trace.csv> [--timed K] [--replays R]
     python -m amd_optimization_challenge_amd.profsum pmc    <fetch counter_collection.csv> <write counter_collection.csv>
     python -m amd_optimization_challenge_amd.profsum sq     <counter_collection.csv> [--match NAME]
+    python -m amd_optimization_challenge_amd.profsum calls  <p_kernel_trace.csv>
 
 trace: per-kernel calls / total / mean / min / max, then every run of at
 least K back-to-back launches of one decode kernel (name and grid): split
@@ -22,6 +23,12 @@ order).
 
 sq: mean of every SQ_ counter per run, as for pmc (``--match S``: the
 kernels whose name contains S instead of the decode kernels).
+
+calls: every whole operator call in the trace (a run of the operator's own
+kernels with one decode launch, ending with the combine, that follows some
+other kernel, such as the flush fill), grouped by its kernels and grids: per position the
+median and minimum duration and the median gap from the previous kernel's
+end, and the median span from the first start to the last end.
 
 Reads only the CSV files rocprofv3 writes (``--output-format csv``).
 """
@@ -191,6 +198,39 @@ def sq_summary(path, match=DECODE):
     return "\n".join(lines)
 
 
+OPERATOR = ("amax_kernel", "quant_fp8_kernel", "plan_kernel") + DECODE + ("combine_kernel",)
+
+
+def calls_summary(path):
+    ks = read_trace(path)
+    calls, cur = [], []
+    for k in ks:
+        if any(o in k["name"] for o in OPERATOR):
+            cur.append(k)
+            if "combine_kernel" in k["name"]:
+                # a whole call holds one decode launch (the bench's decode-only
+                # graphs, many decodes back to back, are not calls)
+                if sum(any(d in x["name"] for d in DECODE) for x in cur) == 1:
+                    calls.append(cur)
+                cur = []
+        else:
+            cur = []
+    groups = collections.OrderedDict()
+    for c in calls:
+        groups.setdefault(tuple((short(k["name"]), k["grid"]) for k in c), []).append(c)
+    lines = []
+    for sig, cs in groups.items():
+        lines += [f"{len(cs)} calls", "", "| # | kernel | grid (threads) | median us | min us | gap before, median us |",
+                  "|---|---|---|---|---|---|"]
+        for i, (name, grid) in enumerate(sig):
+            d = [(c[i]["end"] - c[i]["start"]) / 1e3 for c in cs]
+            gap = f"{statistics.median((c[i]['start'] - c[i - 1]['end']) / 1e3 for c in cs):.2f}" if i else "-"
+            lines.append(f"| {i + 1} | `{name}` | {grid} | {statistics.median(d):.2f} | {min(d):.2f} | {gap} |")
+        span = [(c[-1]["end"] - c[0]["start"]) / 1e3 for c in cs]
+        lines += ["", f"first start to last end: median {statistics.median(span):.2f} us, min {min(span):.2f} us", ""]
+    return "\n".join(lines).rstrip()
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -204,11 +244,15 @@ def main(argv=None) -> int:
     s = sub.add_parser("sq")
     s.add_argument("csv")
     s.add_argument("--match", default=None, help="kernel-name substring (default: the decode kernels)")
+    c = sub.add_parser("calls")
+    c.add_argument("csv")
     a = ap.parse_args(argv)
     if a.cmd == "trace":
         print(trace_summary(a.csv, a.timed, a.replays))
     elif a.cmd == "pmc":
         print(pmc_summary(a.fetch_csv, a.write_csv))
+    elif a.cmd == "calls":
+        print(calls_summary(a.csv))
     else:
         print(sq_summary(a.csv, (a.match,) if a.match else DECODE))
     return 0

@@ -71,3 +71,28 @@ def test_pmc_runs_split_by_set_up_kernels(tmp_path):
     _write(tmp_path / "w.csv", PMC_COLS, rows("WRITE_SIZE", [10.0, 10.0, 10.0, 10.0]))
     out = profsum.pmc_summary(str(tmp_path / "f.csv"), str(tmp_path / "w.csv"))
     assert f"traffic.launch1={(2000 + 10) * 1024}" in out and f"traffic.launch2={(1000 + 10) * 1024}" in out
+
+
+def test_calls_groups_whole_calls_and_skips_decode_only_runs(tmp_path):
+    """Whole calls (flush, then amax, quant, one decode, combine) are grouped
+    by their kernels; a decode-only run followed by a combine is not a call."""
+    rows, t = [], 0
+    for i in range(3):
+        for name, d, gap in [("fill", 50_000, 100), ("mla::amax_kernel(x)", 4000 + 1000 * i, 200),
+                             ("mla::quant_fp8_kernel(x)", 5000, 300), (DEC, 60_000, 400),
+                             ("mla::combine_kernel(x)", 8000, 100)]:
+            rows.append(("KERNEL_DISPATCH", name, t, t + d, 4096))
+            t += d + gap
+    for name, d in [(DEC, 7000), (DEC, 7000), ("mla::combine_kernel(x)", 3000)]:
+        rows.append(("KERNEL_DISPATCH", name, t, t + d, 4096))
+        t += d + 100
+    p = tmp_path / "p_kernel_trace.csv"
+    _write(p, TRACE_COLS, rows)
+    out = profsum.calls_summary(str(p))
+    assert out.count(" calls") == 1 and out.startswith("3 calls"), out
+    amax = [l for l in out.splitlines() if l.startswith("| 1 |")][0]
+    assert [c.strip() for c in amax.split("|")][4:7] == ["5.00", "4.00", "-"], amax
+    dec = [l for l in out.splitlines() if l.startswith("| 3 |")][0]
+    assert [c.strip() for c in dec.split("|")][4:7] == ["60.00", "60.00", "0.30"], dec
+    # span: amax start to combine end = amax + 200 + 5000 + 300 + 60000 + 400 + 8000 (median amax 5000)
+    assert f"median {(5000 + 200 + 5000 + 300 + 60000 + 400 + 8000) / 1e3:.2f} us" in out, out
