@@ -213,7 +213,7 @@ __device__ __forceinline__ int block_exscan(int v, int* red, int* total) {
 // chunk, the item count and the length sums.  Scratch: 256 keys (8 bytes
 // each), 256 counts and kPlanRedInts ints of LDS; it ends with a barrier after
 // its last scratch read.  The chunk is the one-wave plan's (the same search
-// bounds, the same closed form for equal lengths), found four candidates a
+// bounds, the same closed form for equal lengths), found three candidates a
 // round; each reduction round is one barrier, its partials in one of two
 // banks of s_red that alternate, so a bank is rewritten only after every
 // thread has passed the barrier that follows its reads.
